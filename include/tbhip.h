@@ -1,0 +1,113 @@
+/*
+ * libtbhip — C ABI of the MI355X (gfx950) kernel backend "hip".
+ *
+ * Every entry point:
+ *   - takes raw device pointers, int64 sizes and the hipStream_t to launch on;
+ *   - is asynchronous on that stream, allocates no device memory and frees none
+ *     (the caller owns every buffer, including any workspace);
+ *   - is safe to capture into a hipGraph (no synchronisation, no host<->device
+ *     copies, no hipMemset);
+ *   - returns TB_OK or an error code, with a message in tb_last_error() (a
+ *     thread-local string).  Shape or alignment errors are detected on the host
+ *     before anything is launched.
+ *
+ * fp16 and bf16 buffers are passed as uint16_t bit patterns, fp8-e4m3 (OCP
+ * "e4m3fn") as uint8_t codes.  All matrices are row-major and densely packed
+ * unless a parameter says otherwise.
+ *
+ * Int4 weight format ("N-packed, low nibble first"): a logical K x N matrix of
+ * 4-bit codes q in [0, 15] is stored as uint8 [K, N/2]; byte [k, j] holds
+ * q[k, 2j] in bits 0-3 and q[k, 2j+1] in bits 4-7.  Group-wise parameters run
+ * along K with group size G: scales fp16 [K/G, N], zero-points int4 codes
+ * packed the same way as uint8 [K/G, N/2].  The dequantised value is
+ * fp16((q - z) * s): q - z is exact, the product is rounded once (RNE).
+ *
+ * Each declaration names the reference (Tilebench) interface it stands in for.
+ * The reference drives backends through the Python function
+ *     tilebench.benchmarks.operators.<op>.impl_<backend>.run(*inputs, ...)
+ * (tilebench/core/engine.py:347-348); the per-operator Python module
+ * tilebench_amd/benchmarks/operators/<op>/impl_hip.py binds these symbols with
+ * ctypes and keeps that run() signature.
+ */
+#ifndef TBHIP_H
+#define TBHIP_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int tb_status;
+#define TB_OK 0
+#define TB_E_INVALID 1   /* bad shape, size or argument                    */
+#define TB_E_ALIGN 2     /* a pointer is not aligned as the kernel requires */
+#define TB_E_HIP 3       /* a HIP launch or runtime call failed            */
+#define TB_E_WORKSPACE 4 /* workspace missing or too small                 */
+
+/* Library version string, e.g. "tbhip 0.1.0 gfx950". */
+const char* tb_version(void);
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char* tb_last_error(void);
+
+/*
+ * Int4 group-wise weight dequantisation.
+ *   packed uint8 [K, N/2], scales fp16 [K/G, N], zeros uint8 [K/G, N/2]
+ *   -> out fp16 [K, N],  out[k, n] = fp16((q[k,n] - z[k/G, n]) * s[k/G, n]).
+ * Requires N even, K % G == 0.  The vectorised path needs N % 32 == 0 and
+ * 16-byte aligned pointers; other shapes take a scalar path.
+ * Replaces: weight_dequant/impl_triton.py:43 run(X, S, M, N, TILE_SIZE)
+ * (the reference's dequantisation operator, float X times a tile scale).
+ */
+tb_status tb_int4_dequant(const uint8_t* packed, const uint16_t* scales, const uint8_t* zeros,
+                          uint16_t* out, int64_t K, int64_t N, int64_t group, hipStream_t stream);
+
+/*
+ * MoE router gating: per row of logits [M, E], select the
+ * k largest logits (descending; equal logits -> lowest expert index first),
+ * then weights = softmax over the k selected logits, computed in fp32.
+ *   dtype: 0 = fp32, 1 = fp16, 2 = bf16 (logits and weights share it)
+ *   logits [M, E] -> weights [M, k] (dtype), indices int32 [M, k].
+ * Requires 1 <= k <= min(E, 32) and E <= 1024.
+ * Replaces: moe_topk_gating/impl_triton.py:58 run(logits, M, E, k).
+ */
+tb_status tb_moe_topk_gating(const void* logits, void* weights, int32_t* indices, int64_t M,
+                             int64_t E, int64_t k, int dtype, hipStream_t stream);
+
+/*
+ * Per-token fp8-e4m3 activation quantisation (step 1).
+ *   A fp16 [M, K] -> Aq e4m3 codes uint8 [M, K], sa fp32 [M]
+ *   sa[m] = fp32(max_k |A[m,k]|) / 448 (IEEE division),
+ *   Aq[m,k] = e4m3(fp32(A[m,k]) / sa[m]): the quotient rounded to fp32, then
+ *   to e4m3 round-to-nearest-even without saturation (|x| > 464 -> NaN code).
+ *   A row of zeros gives sa = 0 and NaN codes 0xFF (the x86 0/0 result).
+ * Requires K % 8 == 0 and 16-byte aligned A and Aq.
+ * Replaces: quantize_global/impl_triton.py:31 run(x) (the reference's
+ * quantisation operator; it casts to fp16 without scales).
+ */
+tb_status tb_fp8_act_quant(const uint16_t* A, uint8_t* Aq, float* sa, int64_t M, int64_t K,
+                           hipStream_t stream);
+
+/*
+ * Fill `bytes` bytes of `buf` with a 32-bit pattern using a plain store
+ * kernel.  Used to evict the L2 and the 256 MiB MALL between timed launches
+ * (a kernel, not hipMemset, so it may be captured into a graph).
+ * Requires bytes % 16 == 0 and a 16-byte aligned buffer.
+ * Replaces: tilebench/core/timer.py:107 _flush_l2_cache().
+ */
+tb_status tb_l2_flush(void* buf, int64_t bytes, uint32_t pattern, hipStream_t stream);
+
+/*
+ * Calibration probe: streaming copy dst <- src of `bytes` bytes (16-byte
+ * granules, grid-stride), the kernel the measured HBM peak is taken from.
+ * Replaces: tilebench/llm/v2/calibration/gpu_probes.py:284 probe_stream().
+ */
+tb_status tb_probe_copy(const void* src, void* dst, int64_t bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TBHIP_H */

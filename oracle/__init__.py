@@ -1,0 +1,44 @@
+"""CPU oracle for the ``hip`` backend — TEST INFRASTRUCTURE ONLY.
+
+A plain numpy restatement of what each operator on the hot path computes.  It
+is imported only by ``tests/``, by ``__graft_entry__.smoke()`` (as the checker)
+and by the ``cpu_baseline`` leg of ``bench.py`` (as the timed CPU port).  The
+shipped backend (``tilebench_amd``) never imports it and has no CPU fallback.
+
+Reference anchors (Tilebench has no operator for any of these five configs; the
+oracle follows the semantics of the nearest reference operators and the
+BASELINE config text):
+
+* int4 dequant      — weight_dequant/impl_torch.py:4-8 (elementwise X * S[i//T, j//T],
+                      here with int4 codes, zero-points and groups along K);
+                      sub-byte unpack as in matmul_int8/impl_torch.py:10-14.
+* w4a16 GEMM        — matmul_fp32_fp16_fp8/impl_torch.py:21-27 fp16 path (matmul) on
+                      the dequantised weights, fp32 accumulation.
+* fp8 act quant     — dequantize_rowwise/impl_torch.py:4-7 (per-row absmax scale)
+                      inverted, with torch's float -> float8_e4m3fn cast (RNE, no
+                      saturation).
+* fp8 scaled GEMM   — matmul_fp32_fp16_fp8/impl_torch.py:10-26 (_scaled_mm, bf16 out)
+                      with per-row / per-column scales instead of unit scales.
+* MoE gating        — moe_topk_gating/impl_torch.py:4-20 (topk, softmax over the k
+                      values in fp32, int32 indices) with ties -> lowest index.
+
+How each function is pinned (tests/test_oracle.py): closed forms and exact
+rational arithmetic (dequant), the torch CPU fp8 cast over every fp16 value and
+every e4m3 rounding boundary (fp8 codes), brute-force float64 products on small
+inputs and algebraic identities (GEMMs), the reference problem statement's
+worked example, a brute-force ranking and float64 softmax (gating).
+"""
+from .core import (  # noqa: F401
+    bf16_bits_to_f32,
+    e4m3_from_f32,
+    e4m3_to_f32,
+    f32_to_bf16_bits,
+    fp8_act_quant,
+    fp8_scaled_gemm,
+    int4_dequant,
+    moe_topk_gating,
+    moe_w4a16_grouped_gemm,
+    pack_int4,
+    unpack_int4,
+    w4a16_gemm,
+)

@@ -1,0 +1,212 @@
+"""numpy restatement of the hot-path operators (test infrastructure only).
+
+Every function works on host numpy arrays.  fp16 is numpy float16; bf16 and
+fp8-e4m3 are carried as their raw uint16 / uint8 bit patterns.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+# ----------------------------------------------------------------------------- int4 packing
+
+
+def pack_int4(q: np.ndarray) -> np.ndarray:
+    """uint8 codes [..., C] in [0, 15] -> uint8 [..., C/2], low nibble first:
+    byte j = q[2j] | q[2j+1] << 4 (the BASELINE config-0 packing)."""
+    q = np.asarray(q, dtype=np.uint8)
+    if q.shape[-1] % 2:
+        raise ValueError("last dimension must be even")
+    if (q > 15).any():
+        raise ValueError("int4 codes must be in [0, 15]")
+    return (q[..., 0::2] | (q[..., 1::2] << 4)).astype(np.uint8)
+
+
+def unpack_int4(p: np.ndarray) -> np.ndarray:
+    """Inverse of pack_int4: uint8 [..., C/2] -> uint8 codes [..., C]."""
+    p = np.asarray(p, dtype=np.uint8)
+    out = np.empty(p.shape[:-1] + (p.shape[-1] * 2,), dtype=np.uint8)
+    out[..., 0::2] = p & 0x0F
+    out[..., 1::2] = p >> 4
+    return out
+
+
+# ----------------------------------------------------------------------------- int4 dequant
+
+
+def int4_dequant(packed: np.ndarray, scales: np.ndarray, zeros: np.ndarray, group: int) -> np.ndarray:
+    """fp16 [K, N] = fp16((q - z) * s), groups of `group` rows along K.
+
+    packed uint8 [K, N/2]; scales fp16 [K/G, N]; zeros uint8 [K/G, N/2] (packed
+    like the weights).  (q - z) is an exact small integer and its product with an
+    fp16 scale is exact in fp32, so the only rounding is the final fp32 -> fp16
+    (round-to-nearest-even, which numpy's astype implements)."""
+    q = unpack_int4(packed).astype(np.int16)
+    z = unpack_int4(zeros).astype(np.int16)
+    K, N = q.shape
+    if K % group:
+        raise ValueError("K must be a multiple of the group size")
+    s = np.asarray(scales, dtype=np.float16).astype(np.float32)
+    if s.shape != (K // group, N) or z.shape != (K // group, N):
+        raise ValueError("scales / zeros must be [K/G, N]")
+    d = (q.reshape(K // group, group, N) - z[:, None, :]).astype(np.float32)
+    return (d * s[:, None, :]).astype(np.float16).reshape(K, N)
+
+
+# ----------------------------------------------------------------------------- bf16 helpers
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bit pattern, round-to-nearest-even; NaN -> quiet NaN."""
+    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = (b & 0x7FFFFFFF) > 0x7F800000
+    r[nan] = ((b[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# ----------------------------------------------------------------------------- fp8 e4m3
+
+
+def e4m3_from_f32(x: np.ndarray) -> np.ndarray:
+    """fp32 -> OCP fp8-e4m3 ("fn") codes, round-to-nearest-even, no saturation.
+
+    Magnitudes at or above 480 (the first value whose rounding would need the
+    reserved S.1111.111 pattern) and NaN/inf give the NaN code 0x7F; the sign
+    bit is kept.  Values below 2^-6 round onto the subnormal grid 2^-9 * m."""
+    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    sign = ((b >> 24) & 0x80).astype(np.uint8)
+    mag = b & np.uint32(0x7FFFFFFF)
+    out = np.empty(mag.shape, dtype=np.uint8)
+
+    nan = mag >= np.uint32(0x43F00000)
+    sub = mag < np.uint32(121 << 23)
+    nrm = ~(nan | sub)
+
+    out[nan] = 0x7F
+    # subnormal grid: round |x| / 2^-9 to the nearest integer, ties to even
+    # (exact in float64: |x| < 2^-6 has at most 24 significant bits)
+    v = mag[sub].view(np.float32).astype(np.float64) * 512.0
+    out[sub] = np.rint(v).astype(np.uint8)  # np.rint rounds half to even
+    # normal range: keep 3 mantissa bits, RNE on the 20 dropped bits, rebias 127 -> 7
+    m = mag[nrm].astype(np.uint64)
+    kept = m >> 20
+    rem = m & 0xFFFFF
+    up = (rem > 0x80000) | ((rem == 0x80000) & ((kept & 1) == 1))
+    code = kept + up.astype(np.uint64) - (120 << 3)
+    out[nrm] = code.astype(np.uint8)
+    return out | sign
+
+
+_E4M3_TABLE = None
+
+
+def e4m3_to_f32(c: np.ndarray) -> np.ndarray:
+    """fp8-e4m3 codes -> fp32 values (exact)."""
+    global _E4M3_TABLE
+    if _E4M3_TABLE is None:
+        t = np.empty(256, dtype=np.float32)
+        for code in range(256):
+            s = -1.0 if code & 0x80 else 1.0
+            e = (code >> 3) & 0xF
+            m = code & 7
+            if e == 15 and m == 7:
+                t[code] = np.nan
+            elif e == 0:
+                t[code] = s * m * 2.0 ** -9
+            else:
+                t[code] = s * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+        _E4M3_TABLE = t
+    return _E4M3_TABLE[np.asarray(c, dtype=np.uint8)]
+
+
+def fp8_act_quant(A: np.ndarray):
+    """Per-row fp8 quantisation of fp16 A [M, K] -> (codes uint8 [M, K], sa fp32 [M]).
+
+    sa = fp32(max |A[m]|) / 448; codes = e4m3(fp32(A) / sa), both IEEE fp32
+    divisions.  An all-zero row has sa = 0 and every code 0xFF (the NaN with the
+    sign bit that x86 produces for 0/0)."""
+    A = np.asarray(A, dtype=np.float16)
+    amax = np.abs(A).max(axis=1).astype(np.float32)
+    sa = (amax / np.float32(448.0)).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q = (A.astype(np.float32) / sa[:, None]).astype(np.float32)
+    codes = e4m3_from_f32(q)
+    codes[amax == 0] = 0xFF
+    return codes, sa
+
+
+def fp8_scaled_gemm(Aq: np.ndarray, Wq: np.ndarray, sa: np.ndarray, sw: np.ndarray) -> np.ndarray:
+    """Y bf16 bits [M, N] = bf16(sa[m] * sw[n] * sum_k e4m3(Aq[m,k]) * e4m3(Wq[k,n])).
+
+    Aq [M, K] and Wq [K, N] are e4m3 codes (any strides).  The product of two
+    e4m3 values is exact in float64 and K <= 2^16 terms of it sum with error far
+    below the bf16 rounding, so this is the fp32-accumulate result rounded once."""
+    a = e4m3_to_f32(Aq).astype(np.float64)
+    w = e4m3_to_f32(Wq).astype(np.float64)
+    acc = a @ w
+    y = (acc * np.asarray(sa, np.float64)[:, None]) * np.asarray(sw, np.float64)[None, :]
+    return f32_to_bf16_bits(y.astype(np.float32))
+
+
+# ----------------------------------------------------------------------------- W4A16 GEMMs
+
+
+def w4a16_gemm(A: np.ndarray, packed: np.ndarray, scales: np.ndarray, zeros: np.ndarray, group: int) -> np.ndarray:
+    """fp16 [M, N] = fp16(A @ dequant(W)) with fp32 accumulation."""
+    W = int4_dequant(packed, scales, zeros, group).astype(np.float32)
+    return (np.asarray(A, dtype=np.float16).astype(np.float32) @ W).astype(np.float16)
+
+
+def moe_w4a16_grouped_gemm(A: np.ndarray, packed: np.ndarray, scales: np.ndarray, zeros: np.ndarray,
+                           offsets: np.ndarray, group: int) -> np.ndarray:
+    """Grouped W4A16: rows offsets[e]:offsets[e+1] of A use expert e's weights.
+
+    A fp16 [R, K]; packed uint8 [E, K, N/2]; scales fp16 [E, K/G, N]; zeros uint8
+    [E, K/G, N/2]; offsets int [E+1], non-decreasing, offsets[0] = 0,
+    offsets[E] = R.  Returns fp16 [R, N]."""
+    E = packed.shape[0]
+    off = np.asarray(offsets, dtype=np.int64)
+    if off.shape != (E + 1,) or off[0] != 0 or off[-1] != A.shape[0] or (np.diff(off) < 0).any():
+        raise ValueError("offsets must be [E+1], non-decreasing, from 0 to R")
+    N = packed.shape[2] * 2
+    Y = np.zeros((A.shape[0], N), dtype=np.float16)
+    for e in range(E):
+        lo, hi = off[e], off[e + 1]
+        if hi > lo:
+            Y[lo:hi] = w4a16_gemm(A[lo:hi], packed[e], scales[e], zeros[e], group)
+    return Y
+
+
+# ----------------------------------------------------------------------------- MoE gating
+
+
+def moe_topk_gating(logits: np.ndarray, k: int, dtype: str = "fp32"):
+    """Top-k gating of logits [M, E] -> (weights [M, k], indices int32 [M, k]).
+
+    Order: logits descending, NaN above everything, equal logits (including
+    -0.0 == +0.0) by ascending expert index.  Weights: softmax over the k
+    selected logits in fp32, returned in the logits' dtype.  `dtype` is "fp32",
+    "fp16" or "bf16"; bf16 logits and weights are uint16 bit patterns."""
+    if dtype == "bf16":
+        x = bf16_bits_to_f32(logits)
+    else:
+        x = np.asarray(logits).astype(np.float32)
+    M, E = x.shape
+    if not 1 <= k <= E:
+        raise ValueError("need 1 <= k <= E")
+    idx = np.broadcast_to(np.arange(E), (M, E))
+    isnan = np.isnan(x)
+    v = np.where(isnan, 0.0, x).astype(np.float64) + 0.0  # + 0.0 folds -0.0 onto +0.0
+    order = np.lexsort((idx, -v, ~isnan), axis=-1)[:, :k]
+    vals = np.take_along_axis(x, order, axis=1).astype(np.float32)
+    e = np.exp(vals - vals[:, :1]).astype(np.float32)
+    w = (e / e.sum(axis=1, keepdims=True, dtype=np.float32)).astype(np.float32)
+    if dtype == "fp16":
+        w = w.astype(np.float16)
+    elif dtype == "bf16":
+        w = f32_to_bf16_bits(w)
+    return w, order.astype(np.int32)

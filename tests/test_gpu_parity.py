@@ -1,0 +1,152 @@
+"""GPU parity of every hip kernel against the CPU oracle (seeded inputs).
+
+Bit-exact for dequantised values, fp8 codes, fp32 scales and top-k indices;
+gating weights within 1e-5.  Each case prints its name and shape before the GPU
+call so that a failing run names its case.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tilebench_amd.data import tensors as T
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print("[gpu case]", *a, flush=True)
+
+
+def _u16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+# ----------------------------------------------------------------------------- int4 dequant
+
+@pytest.mark.parametrize("K,N,G", [(4096, 4096, 128), (256, 512, 128), (128, 32, 64), (64, 6, 32), (128, 4096, 32)])
+def test_int4_dequant_matches_oracle(gpu, K, N, G):
+    from tilebench_amd.benchmarks.operators.int4_dequant import impl_hip
+
+    _say("int4_dequant", K, N, G)
+    p, s, z, K, N, G = T.generate_int4_dequant_inputs(K, N, G, seed=K + N, device="cpu")
+    out = impl_hip.run(p.to(gpu), s.to(gpu), z.to(gpu), K, N, G)
+    torch.cuda.synchronize()
+    ref = oracle.int4_dequant(p.numpy(), s.numpy(), z.numpy(), G)
+    np.testing.assert_array_equal(_u16(out), ref.view(np.uint16))
+
+
+def test_int4_dequant_exhaustive_codes(gpu):
+    """Every (q, z) pair against every scale of a spread of fp16 scales (incl. negative and subnormal)."""
+    from tilebench_amd.benchmarks.operators.int4_dequant import impl_hip
+
+    _say("int4_dequant exhaustive")
+    K, N, G = 256, 256, 16   # 16 groups; within a group rows cover q = 0..15
+    q = np.tile(np.arange(16, dtype=np.uint8)[:, None], (K // 16, N))          # row r -> q = r % 16
+    zc = np.tile(np.arange(16, dtype=np.uint8), (K // G, N // 16))              # col n -> z = n % 16
+    rng = np.random.default_rng(7)
+    sbits = rng.integers(0, 0x7C00, size=(K // G, N), dtype=np.uint16)          # every finite magnitude band
+    sbits[rng.random((K // G, N)) < 0.5] |= 0x8000
+    scales = sbits.view(np.float16)
+    packed, zeros = oracle.pack_int4(q), oracle.pack_int4(zc)
+    out = impl_hip.run(torch.from_numpy(packed).to(gpu), torch.from_numpy(scales.copy()).to(gpu),
+                       torch.from_numpy(zeros).to(gpu), K, N, G)
+    torch.cuda.synchronize()
+    ref = oracle.int4_dequant(packed, scales, zeros, G)
+    np.testing.assert_array_equal(_u16(out), ref.view(np.uint16))
+
+
+# ----------------------------------------------------------------------------- gating
+
+@pytest.mark.parametrize("M,E,k,dist", [(16384, 64, 8, "normal"), (16384, 256, 8, "normal"), (1000, 128, 2, "grid"),
+                                        (333, 20, 5, "normal"), (64, 1024, 32, "normal"), (7, 8, 8, "normal"),
+                                        (100, 512, 8, "normal"), (65, 100, 3, "normal")])
+def test_gating_matches_oracle(gpu, M, E, k, dist):
+    from tilebench_amd.benchmarks.operators.moe_topk_gating import impl_hip
+
+    _say("gating", M, E, k, dist)
+    logits, M, E, k = T.generate_moe_topk_gating_inputs(M, E, k, dist=dist, seed=M + E, device="cpu")
+    w, i = impl_hip.run(logits.to(gpu), M, E, k)
+    torch.cuda.synchronize()
+    rw, ri = oracle.moe_topk_gating(logits.numpy(), k)
+    np.testing.assert_array_equal(i.cpu().numpy(), ri)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, atol=1e-5, rtol=1e-5)
+
+
+def test_gating_ties_nan_signed_zero(gpu):
+    from tilebench_amd.benchmarks.operators.moe_topk_gating import impl_hip
+
+    _say("gating ties")
+    rng = np.random.default_rng(3)
+    x = rng.integers(-3, 4, size=(512, 64)).astype(np.float32)   # heavy ties
+    x[5, 10] = -0.0
+    x[6, :] = 0.0
+    x[6, 7] = -0.0
+    x[7, 3] = np.nan
+    x[8, :] = -np.inf
+    x[9, 60] = np.inf
+    w, i = impl_hip.run(torch.from_numpy(x).to(gpu), 512, 64, 8)
+    torch.cuda.synchronize()
+    rw, ri = oracle.moe_topk_gating(x, 8)
+    np.testing.assert_array_equal(i.cpu().numpy(), ri)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, atol=1e-5, rtol=1e-5, equal_nan=True)
+
+
+@pytest.mark.parametrize("dt", ["fp16", "bf16"])
+def test_gating_half_dtypes(gpu, dt):
+    from tilebench_amd.benchmarks.operators.moe_topk_gating import impl_hip
+    from tilebench_amd.benchmarks.operators.moe_topk_gating import impl_torch
+
+    _say("gating", dt)
+    tdt = torch.float16 if dt == "fp16" else torch.bfloat16
+    logits, M, E, k = T.generate_moe_topk_gating_inputs(2048, 128, 2, dtype=tdt, dist="grid", seed=11, device="cpu")
+    w, i = impl_hip.run(logits.to(gpu), M, E, k)
+    torch.cuda.synchronize()
+    bits = logits.view(torch.int16).numpy().view(np.uint16) if dt == "bf16" else logits.numpy()
+    rw, ri = oracle.moe_topk_gating(bits, k, dtype=dt)
+    np.testing.assert_array_equal(i.cpu().numpy(), ri)
+    np.testing.assert_array_equal(_u16(w), np.asarray(rw).view(np.uint16))
+    tw, ti = impl_torch.run(logits, M, E, k)   # the harness reference agrees too
+    np.testing.assert_array_equal(ti.numpy(), ri)
+
+
+# ----------------------------------------------------------------------------- fp8 quant
+
+@pytest.mark.parametrize("M,K", [(8192, 8192), (64, 1024), (3, 24), (17, 2048 * 3), (5, 40000), (256, 16384)])
+def test_fp8_quant_matches_oracle(gpu, M, K):
+    from tilebench_amd.benchmarks.operators.fp8_act_quant import impl_hip
+
+    _say("fp8_act_quant", M, K)
+    (A,) = T.generate_fp8_act_quant_inputs(M, K, seed=M + K, device="cpu")
+    q, sa = impl_hip.run(A.to(gpu))
+    torch.cuda.synchronize()
+    rq, rsa = oracle.fp8_act_quant(A.numpy())
+    np.testing.assert_array_equal(sa.cpu().numpy().view(np.uint32), rsa.view(np.uint32))
+    got = q.cpu().view(torch.uint8).numpy()
+    bad = np.argwhere(got != rq)
+    assert bad.size == 0, f"{len(bad)} codes differ, first {bad[:3].tolist()}"
+
+
+def test_fp8_quant_special_rows(gpu):
+    """Zero row, a row whose max maps to exactly 448, subnormal fp16 inputs, +-65504, signed zeros."""
+    from tilebench_amd.benchmarks.operators.fp8_act_quant import impl_hip
+
+    _say("fp8_act_quant special rows")
+    K = 4096
+    rng = np.random.default_rng(5)
+    A = rng.standard_normal((8, K)).astype(np.float16)
+    A[0] = 0
+    A[1, 17] = 448.0
+    A[2] = (np.arange(K) % 1024).astype(np.uint16).view(np.float16)        # subnormals and small normals
+    A[3, ::2] = np.float16(65504.0)
+    A[3, 1::2] = np.float16(-65504.0)
+    A[4] = -0.0
+    A[4, 9] = 1.0
+    A[5] = np.arange(K, dtype=np.uint16).view(np.float16)                    # every bit pattern below 0x1000
+    A[6] = (np.arange(K, dtype=np.uint32) * 15 + 0x3C00).astype(np.uint16).view(np.float16)
+    A[6][~np.isfinite(A[6])] = 1.0
+    q, sa = impl_hip.run(torch.from_numpy(A).to(gpu))
+    torch.cuda.synchronize()
+    rq, rsa = oracle.fp8_act_quant(A)
+    np.testing.assert_array_equal(sa.cpu().numpy().view(np.uint32), rsa.view(np.uint32))
+    np.testing.assert_array_equal(q.cpu().view(torch.uint8).numpy(), rq)

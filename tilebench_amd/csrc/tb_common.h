@@ -1,0 +1,72 @@
+// Shared device/host helpers for libtbhip (gfx950 / CDNA4 only).
+//
+// Everything here is written for 64-lane wavefronts. Host-side helpers record
+// a thread-local error message that tb_last_error() returns; entry points never
+// print, abort or allocate device memory.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+
+#include "tbhip.h"
+
+namespace tb {
+
+// ---------------------------------------------------------------- host errors
+void set_error(const char* fmt, ...);
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+#define TB_CHECK_ARG(cond, ...)                         \
+  do {                                                  \
+    if (!(cond)) {                                      \
+      ::tb::set_error(__VA_ARGS__);                     \
+      return TB_E_INVALID;                              \
+    }                                                   \
+  } while (0)
+
+#define TB_CHECK_ALIGN(ptr, a, name)                                                    \
+  do {                                                                                  \
+    if (!::tb::aligned((ptr), (a))) {                                                   \
+      ::tb::set_error("%s must be %d-byte aligned (got %p)", (name), (int)(a), (ptr));  \
+      return TB_E_ALIGN;                                                                \
+    }                                                                                   \
+  } while (0)
+
+// Report the status of the launch that was just enqueued.
+inline tb_status launch_status(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return TB_E_HIP;
+  }
+  return TB_OK;
+}
+
+// ------------------------------------------------------------- device helpers
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Non-temporal 16-byte global load/store: streamed data is read once, so it
+// should not evict reused data (scales, zero-points) from L2.
+__device__ __forceinline__ u32x4 ld_nt(const u32x4* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ void st_nt(u32x4* p, u32x4 v) { __builtin_nontemporal_store(v, p); }
+
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+__device__ __forceinline__ f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
+__device__ __forceinline__ uint32_t as_u32(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// Two int4 codes (in bytes 0 and 2 of `pair`, values 0..15) to a half2 holding
+// 1024 + code: 0x6400 is 1024.0 in fp16 and its ulp is 1, so OR-ing the code
+// into the mantissa is an exact conversion.
+__device__ __forceinline__ f16x2 magic_h2(uint32_t pair) { return as_h2(pair | 0x64006400u); }
+
+}  // namespace tb

@@ -1,0 +1,75 @@
+// Library-level entry points: version, error reporting, the cache-flush fill
+// kernel and the HBM streaming-copy probe.
+#include "tb_common.h"
+
+#include <string.h>
+
+namespace tb {
+
+static thread_local char g_last_error[512] = {0};
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+}
+
+// Grid-stride store of a 16-byte pattern.
+__global__ void __launch_bounds__(256) fill_kernel(u32x4* __restrict__ dst, int64_t n16, uint32_t pattern) {
+  const u32x4 v = {pattern, pattern, pattern, pattern};
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) st_nt(dst + i, v);
+}
+
+// Grid-stride copy, 4 independent 16-byte loads in flight per thread.
+__global__ void __launch_bounds__(256) copy_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                   int64_t n16) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    u32x4 a = ld_nt(src + i), b = ld_nt(src + i + stride), c = ld_nt(src + i + 2 * stride),
+          d = ld_nt(src + i + 3 * stride);
+    st_nt(dst + i, a);
+    st_nt(dst + i + stride, b);
+    st_nt(dst + i + 2 * stride, c);
+    st_nt(dst + i + 3 * stride, d);
+  }
+  for (; i < n16; i += stride) st_nt(dst + i, ld_nt(src + i));
+}
+
+static int grid_for(int64_t n16) {
+  // 256 CUs x 8 resident 256-thread blocks; never more blocks than granules.
+  int64_t blocks = (n16 + 255) / 256;
+  if (blocks > 2048) blocks = 2048;
+  return (int)(blocks < 1 ? 1 : blocks);
+}
+
+}  // namespace tb
+
+extern "C" {
+
+const char* tb_version(void) { return "tbhip 0.1.0 gfx950"; }
+
+const char* tb_last_error(void) { return tb::g_last_error; }
+
+tb_status tb_l2_flush(void* buf, int64_t bytes, uint32_t pattern, hipStream_t stream) {
+  TB_CHECK_ARG(buf != nullptr && bytes > 0 && bytes % 16 == 0, "tb_l2_flush: bytes must be a positive multiple of 16");
+  TB_CHECK_ALIGN(buf, 16, "buf");
+  const int64_t n16 = bytes / 16;
+  hipLaunchKernelGGL(tb::fill_kernel, dim3(tb::grid_for(n16)), dim3(256), 0, stream,
+                     reinterpret_cast<tb::u32x4*>(buf), n16, pattern);
+  return tb::launch_status("tb_l2_flush");
+}
+
+tb_status tb_probe_copy(const void* src, void* dst, int64_t bytes, hipStream_t stream) {
+  TB_CHECK_ARG(src && dst && bytes > 0 && bytes % 16 == 0, "tb_probe_copy: bytes must be a positive multiple of 16");
+  TB_CHECK_ALIGN(src, 16, "src");
+  TB_CHECK_ALIGN(dst, 16, "dst");
+  const int64_t n16 = bytes / 16;
+  hipLaunchKernelGGL(tb::copy_kernel, dim3(tb::grid_for(n16)), dim3(256), 0, stream,
+                     reinterpret_cast<const tb::u32x4*>(src), reinterpret_cast<tb::u32x4*>(dst), n16);
+  return tb::launch_status("tb_probe_copy");
+}
+
+}  // extern "C"

@@ -1,0 +1,122 @@
+"""ctypes binding of libtbhip.so, the C ABI declared in include/tbhip.h.
+
+The library is built in-tree (``python -m tilebench_amd.build``) and loaded on
+first use.  Nothing here falls back to another implementation: a missing
+library, a missing symbol or a host without a gfx950 device raises, so a caller
+never silently measures or verifies something else.
+
+Every entry point is called with raw ``data_ptr()`` values and the HIP stream
+of the current torch stream; a non-zero status raises ``RuntimeError`` carrying
+the library's own message (``tb_last_error``), or ``ValueError`` for shape and
+alignment errors (the reference engine treats both as a failed backend,
+tilebench/core/engine.py:361-366).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libtbhip.so"
+
+TB_OK = 0
+TB_E_INVALID = 1
+TB_E_ALIGN = 2
+TB_E_HIP = 3
+TB_E_WORKSPACE = 4
+
+_c_i64 = ctypes.c_int64
+_c_p = ctypes.c_void_p
+_c_int = ctypes.c_int
+_c_u32 = ctypes.c_uint32
+
+#: symbol -> argtypes (every entry point returns an int status).
+SIGNATURES: dict[str, list] = {
+    "tb_int4_dequant": [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p],
+    "tb_moe_topk_gating": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p],
+    "tb_fp8_act_quant": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_p],
+    "tb_l2_flush": [_c_p, _c_i64, _c_u32, _c_p],
+    "tb_probe_copy": [_c_p, _c_p, _c_i64, _c_p],
+}
+
+#: symbols returning a C string
+STRING_SYMBOLS = ("tb_version", "tb_last_error")
+
+_lib = None
+
+
+class HipBackendUnavailable(ImportError):
+    """libtbhip.so is missing or cannot run here (no gfx950 device)."""
+
+
+def load_library(path: str | os.PathLike | None = None) -> ctypes.CDLL:
+    """Load libtbhip.so and declare its signatures (no GPU needed)."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise HipBackendUnavailable(
+            f"{p} is not built; run `python -m tilebench_amd.build` (or __graft_entry__.build())")
+    lib = ctypes.CDLL(str(p))
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_int
+    for name in STRING_SYMBOLS:
+        fn = getattr(lib, name)
+        fn.argtypes = []
+        fn.restype = ctypes.c_char_p
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def version() -> str:
+    return load_library().tb_version().decode()
+
+
+def check(status: int, what: str) -> None:
+    """Raise on a non-zero status with the library's message."""
+    if status == TB_OK:
+        return
+    msg = load_library().tb_last_error().decode(errors="replace")
+    if status in (TB_E_INVALID, TB_E_ALIGN, TB_E_WORKSPACE):
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg} (status {status})")
+
+
+_device_checked = False
+
+
+def require_device() -> None:
+    """Fail loudly unless the current device is a gfx950 GPU."""
+    global _device_checked
+    if _device_checked:
+        return
+    import torch
+
+    if not torch.cuda.is_available() or not torch.version.hip:
+        raise HipBackendUnavailable("the hip backend needs a ROCm GPU (torch.cuda is unavailable)")
+    arch = (getattr(torch.cuda.get_device_properties(torch.cuda.current_device()), "gcnArchName", "") or "")
+    if not arch.startswith("gfx950"):
+        raise HipBackendUnavailable(f"libtbhip.so is built for gfx950, the device is {arch!r}")
+    _device_checked = True
+
+
+def stream_handle(device=None) -> int:
+    """Raw hipStream_t of torch's current stream."""
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point with (already converted) arguments and check it."""
+    lib = load_library()
+    check(getattr(lib, name)(*args), name)
+
+
+def ptr(t) -> int:
+    """data_ptr of a tensor (0 for None)."""
+    return 0 if t is None else t.data_ptr()
