@@ -3,9 +3,11 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--op NAME] [--no-cpu-baseline]
 
 A step is one launch of the operator on one batch of seeded synthetic input
-already resident in HBM.  W untimed warmup steps, then exactly K steps between
-two hipEvents on the stream the kernels run on (bracketed by
-torch.cuda.synchronize()).  Prints ONE JSON line with the driver's fields plus:
+already resident in HBM.  W untimed warmup steps, then exactly K steps captured
+into one hipGraph and replayed between two hipEvents on the stream the kernels
+run on (bracketed by torch.cuda.synchronize()).  Steps rotate over copies of
+the input at distinct addresses, together larger than 2x the 256 MiB MALL, so
+no step finds its operands in the last-level cache.  Prints ONE JSON line with the driver's fields plus:
 
   roofline      achieved GB/s or TFLOP/s of the operator's kernel (algorithmic
                 bytes or flops per launch / mean launch time from the events),
@@ -106,33 +108,121 @@ def _w_fp8_quant():
                 cpu_sample=cpu_sample)
 
 
+def _w_w4a16(M):
+    def make():
+        from tilebench_amd.data import tensors as T
+        from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip
+
+        K, N, G = 4096, 11008, 128
+        flops = 2 * M * K * N
+        nbytes = 2 * M * K + K * N // 2 + (K // G) * N * 2 + (K // G) * N // 2 + 2 * M * N
+
+        def inputs():
+            return T.generate_w4a16_gemm_inputs(M, K, N, G, seed=1, device="cuda")
+
+        def cpu_sample():
+            import oracle
+            rows = min(M, 64)
+            A, p, s, z, _ = T.generate_w4a16_gemm_inputs(rows, K, N, G, seed=1, device="cpu")
+            A, p, s, z = A.numpy(), p.numpy(), s.numpy(), z.numpy()
+            work = 2 * rows * K * N if M > 16 else nbytes
+            return ((lambda: oracle.w4a16_gemm(A, p, s, z, G)), work,
+                    f"{rows} of {M} rows (numpy int4 dequant + fp32 BLAS matmul)")
+
+        big = M > 16
+        return dict(name=f"w4a16_gemm_M{M}",
+                    config={"workload": "w4a16_gemm", "M": M, "K": K, "N": N, "group": G},
+                    metric="W4A16 GEMM throughput" if big else "W4A16 decode GEMM HBM throughput",
+                    unit="TFLOP/s" if big else "GB/s", dtype="fp16 x int4 -> fp16 (fp32 acc)",
+                    bound="mfma" if big else "hbm", peak_key="fp16", bytes=nbytes, flops=flops, out_bytes=2 * M * N,
+                    inputs=inputs, step=lambda x: impl_hip.run(*x),
+                    kernel="w4a16_prefill" if big else "w4a16_decode", cpu_sample=cpu_sample)
+    return make
+
+
+def _w_copy():
+    import torch
+
+    nbytes = 1 << 30
+
+    def inputs():
+        return (torch.empty(nbytes // 2, dtype=torch.uint8, device="cuda"),)
+
+    def step(x):
+        from tilebench_amd import runtime as rt
+        src = x[0]
+        dst = torch.empty_like(src)
+        rt.call("tb_probe_copy", src.data_ptr(), dst.data_ptr(), src.numel(), rt.stream_handle())
+        return dst
+
+    return dict(name="hbm_copy_probe", config={"workload": "hbm_copy_probe", "bytes": nbytes},
+                metric="HBM streaming copy (calibration probe)", unit="GB/s", dtype="u8", bound="hbm", bytes=nbytes,
+                flops=None, out_bytes=nbytes // 2, inputs=inputs, step=step, kernel="copy_kernel", cpu_sample=None)
+
+
 WORKLOADS = {
+    "w4a16_gemm_M4096": _w_w4a16(4096),
+    "w4a16_gemm_M16": _w_w4a16(16),
+    "w4a16_gemm_M1": _w_w4a16(1),
     "int4_dequant": _w_int4_dequant,
     "moe_topk_gating_E64": _w_gating(64),
     "moe_topk_gating_E256": _w_gating(256),
     "fp8_act_quant": _w_fp8_quant,
+    "hbm_copy_probe": _w_copy,
 }
-DEFAULT_OP = "int4_dequant"
+DEFAULT_OP = "w4a16_gemm_M4096"
 
 
 # ----------------------------------------------------------------------------- measurement
 
-def time_steps(w, x, steps: int, warmup: int):
-    """Mean ms per step over `steps` back-to-back launches (events on the launch stream)."""
+MALL_BYTES = 256 * 1024 * 1024
+
+
+def _footprint(x) -> int:
+    import torch
+    return sum(t.numel() * t.element_size() for t in x if isinstance(t, torch.Tensor))
+
+
+def input_sets(w, x) -> list:
+    """The inputs plus device copies at other addresses, enough that one pass
+    over all sets moves more than 2x the 256 MiB MALL: consecutive steps then
+    never find their operands in the cache (the reference evicts the LLC
+    before every timed launch, tilebench/core/timer.py:81-117)."""
+    import torch
+    per_set = _footprint(x) + w.get("out_bytes", 0)
+    n = max(1, min(64, -(-2 * MALL_BYTES // max(per_set, 1))))
+    sets = [x]
+    for _ in range(n - 1):
+        sets.append(tuple(t.clone() if isinstance(t, torch.Tensor) else t for t in x))
+    return sets
+
+
+def time_steps(w, sets, steps: int, warmup: int):
+    """Mean ms per step: `steps` launches captured into one hipGraph (no host
+    work between launches), replayed between two hipEvents on the stream the
+    kernels are launched on.  Step i uses input set i mod len(sets) and writes
+    a fresh output buffer."""
     import torch
 
-    for _ in range(warmup):
-        w["step"](x)
+    for i in range(max(1, warmup)):
+        w["step"](sets[i % len(sets)])
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    keep = []
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            keep.append(w["step"](sets[i % len(sets)]))
+    graph.replay()  # upload + warm the instruction cache
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     start.record(stream)
-    for _ in range(steps):
-        w["step"](x)
+    graph.replay()
     stop.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(stop) / steps
+    ms = start.elapsed_time(stop) / steps
+    del keep, graph
+    return ms
 
 
 def roofline(w, ms: float) -> dict:
@@ -169,13 +259,13 @@ def measure(name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
     import torch
 
     w = WORKLOADS[name]()
-    x = w["inputs"]()
+    sets = input_sets(w, w["inputs"]())
     torch.cuda.synchronize()
-    ms = time_steps(w, x, steps, warmup)
-    out = {"name": w["name"], "w": w, "ms": ms, "roofline": roofline(w, ms)}
-    if with_cpu:
+    ms = time_steps(w, sets, steps, warmup)
+    out = {"name": w["name"], "w": w, "ms": ms, "roofline": roofline(w, ms), "input_sets": len(sets)}
+    if with_cpu and w.get("cpu_sample"):
         out["cpu_baseline"] = cpu_baseline(w)
-    del x
+    del sets
     torch.cuda.empty_cache()
     return out
 
@@ -210,7 +300,7 @@ def main(argv=None) -> int:
         "metric": w["metric"], "value": value, "unit": w["unit"], "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": w["dtype"], "data": "synthetic (seeded CPU generator, resident in HBM)",
-        "config": w["config"], "roofline": main_res["roofline"],
+        "config": {**w["config"], "input_sets": main_res["input_sets"]}, "roofline": main_res["roofline"],
         "cpu_baseline": main_res.get("cpu_baseline"),
     }
     if args.suite:

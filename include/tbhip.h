@@ -56,8 +56,8 @@ const char* tb_last_error(void);
  * Int4 group-wise weight dequantisation.
  *   packed uint8 [K, N/2], scales fp16 [K/G, N], zeros uint8 [K/G, N/2]
  *   -> out fp16 [K, N],  out[k, n] = fp16((q[k,n] - z[k/G, n]) * s[k/G, n]).
- * Requires N even, K % G == 0.  The vectorised path needs N % 32 == 0 and
- * 16-byte aligned pointers; other shapes take a scalar path.
+ * Requires N even, K % G == 0.  The vectorised path needs N % 8 == 0,
+ * G % 8 == 0 and 16-byte aligned pointers; other shapes take a scalar path.
  * Replaces: weight_dequant/impl_triton.py:43 run(X, S, M, N, TILE_SIZE)
  * (the reference's dequantisation operator, float X times a tile scale).
  */
@@ -89,6 +89,28 @@ tb_status tb_moe_topk_gating(const void* logits, void* weights, int32_t* indices
  */
 tb_status tb_fp8_act_quant(const uint16_t* A, uint8_t* Aq, float* sa, int64_t M, int64_t K,
                            hipStream_t stream);
+
+/*
+ * W4A16 GEMM: Y = fp16(A @ dequant(W)), fp32 accumulation.
+ *   A fp16 [M, K], W int4 [K, N] (packed uint8 [K, N/2]), scales fp16 [K/G, N],
+ *   zeros uint8 [K/G, N/2] -> Y fp16 [M, N].  Dequantised values are exactly
+ *   those of tb_int4_dequant.
+ * Requires N % 8 == 0, K % 64 == 0, G % 64 == 0, K % G == 0; A, scales 16-byte
+ * aligned.  M <= 16 runs a split-K decode kernel that needs the workspace
+ * reported by tb_w4a16_workspace_size (256-byte aligned; zero-filled once when
+ * allocated: the kernel leaves its counters at zero after every call, so one
+ * workspace serves consecutive calls on one stream; calls that overlap in time
+ * must not share a workspace).  Larger M runs the MFMA prefill kernel and
+ * needs no workspace.
+ * Replaces: matmul_fp32_fp16_fp8/impl_triton.py:124 run(a, b) (the reference's
+ * fp16 GEMM operator), with the weight operand kept int4 in HBM.
+ */
+tb_status tb_w4a16_gemm(const uint16_t* A, const uint8_t* W, const uint16_t* scales, const uint8_t* zeros,
+                        uint16_t* Y, int64_t M, int64_t N, int64_t K, int64_t group, void* workspace,
+                        int64_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes tb_w4a16_gemm needs for this shape (0 if none). */
+tb_status tb_w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int64_t group, int64_t* bytes);
 
 /*
  * Fill `bytes` bytes of `buf` with a 32-bit pattern using a plain store

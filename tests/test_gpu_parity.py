@@ -150,3 +150,59 @@ def test_fp8_quant_special_rows(gpu):
     rq, rsa = oracle.fp8_act_quant(A)
     np.testing.assert_array_equal(sa.cpu().numpy().view(np.uint32), rsa.view(np.uint32))
     np.testing.assert_array_equal(q.cpu().view(torch.uint8).numpy(), rq)
+
+
+# ----------------------------------------------------------------------------- W4A16 GEMM
+
+def _w4a16_check(gpu, M, K, N, G, seed):
+    from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip
+
+    _say("w4a16_gemm", M, K, N, G)
+    A, p, s, z, G = T.generate_w4a16_gemm_inputs(M, K, N, G, seed=seed, device="cpu")
+    Y = impl_hip.run(A.to(gpu), p.to(gpu), s.to(gpu), z.to(gpu), G)
+    torch.cuda.synchronize()
+    ref = oracle.w4a16_gemm(A.numpy(), p.numpy(), s.numpy(), z.numpy(), G)
+    got = Y.cpu().numpy()
+    np.testing.assert_allclose(got.astype(np.float32), ref.astype(np.float32), atol=1e-2, rtol=1e-2)
+    return got, ref
+
+
+@pytest.mark.parametrize("M,K,N,G", [(1, 4096, 11008, 128), (16, 4096, 11008, 128), (256, 512, 512, 128),
+                                     (300, 256, 264, 64), (7, 1024, 1000, 128), (16, 64, 8, 64), (1, 128, 2048, 128),
+                                     (512, 4096, 1024, 128), (33, 384, 392, 128)])
+def test_w4a16_gemm_matches_oracle(gpu, M, K, N, G):
+    _w4a16_check(gpu, M, K, N, G, seed=M + N)
+
+
+def test_w4a16_gemm_full_prefill(gpu):
+    """BASELINE config 1 at M = 4096: checked against the oracle on a row sample
+    (the full fp32 CPU product takes minutes) and for finiteness everywhere."""
+    from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip
+
+    M, K, N, G = 4096, 4096, 11008, 128
+    _say("w4a16_gemm full prefill", M, K, N, G)
+    A, p, s, z, G = T.generate_w4a16_gemm_inputs(M, K, N, G, seed=1, device="cpu")
+    Y = impl_hip.run(A.to(gpu), p.to(gpu), s.to(gpu), z.to(gpu), G)
+    torch.cuda.synchronize()
+    Yc = Y.cpu().numpy()
+    assert np.isfinite(Yc.astype(np.float32)).all()
+    rows = np.random.default_rng(0).choice(M, 96, replace=False)
+    ref = oracle.w4a16_gemm(A.numpy()[rows], p.numpy(), s.numpy(), z.numpy(), G)
+    np.testing.assert_allclose(Yc[rows].astype(np.float32), ref.astype(np.float32), atol=1e-2, rtol=1e-2)
+
+
+def test_w4a16_decode_repeat_calls_reuse_workspace(gpu):
+    """The split-K counters must be back at zero after each call: three calls in a row agree."""
+    from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip
+
+    _say("w4a16_gemm decode repeat")
+    A, p, s, z, G = T.generate_w4a16_gemm_inputs(16, 4096, 11008, 128, seed=5, device="cpu")
+    args = (A.to(gpu), p.to(gpu), s.to(gpu), z.to(gpu), G)
+    outs = [impl_hip.run(*args) for _ in range(3)]
+    torch.cuda.synchronize()
+    first = outs[0].cpu()
+    for i, o in enumerate(outs[1:], 1):
+        diff = (o.cpu().view(torch.int16) != first.view(torch.int16)).nonzero()
+        assert diff.numel() == 0, (f"call {i}: {diff.shape[0]} outputs differ from call 0, first "
+                                   f"{diff[:4].tolist()}: {[float(o[m, n]) for m, n in diff[:4].tolist()]} vs "
+                                   f"{[float(first[m, n]) for m, n in diff[:4].tolist()]}")

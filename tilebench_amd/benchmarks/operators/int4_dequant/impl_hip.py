@@ -25,8 +25,8 @@ def run(packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, K: int,
     out = torch.empty((K, N), dtype=torch.float16, device=packed.device)
     rt.call("tb_int4_dequant", packed.data_ptr(), scales.data_ptr(), zeros.data_ptr(), out.data_ptr(),
             K, N, group, rt.stream_handle(packed.device))
-    _last_config = {"kernel": "int4_dequant_vec" if N % 32 == 0 and group % 4 == 0 else "int4_dequant_scalar",
-                    "rows_per_thread": 4, "cols_per_thread": 32}
+    _last_config = {"kernel": "int4_dequant_vec" if N % 8 == 0 and group % 8 == 0 else "int4_dequant_scalar",
+                    "rows_per_thread": 8, "cols_per_thread": 8}
     return out
 
 

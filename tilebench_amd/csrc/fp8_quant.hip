@@ -12,7 +12,7 @@
 // Division.  Per element the quotient x / sa is formed as
 //   q0 = RN(x * y) with y = RN(1 / sa) computed once per row by an IEEE divide,
 //   r  = fma(-q0, sa, x)   (exact remainder),   q = RN(q0 + r * y)  (fma),
-// the reciprocal-refinement scheme of Markstein (IBM J. Res. Dev. 34(1), 1990).
+// with the sign of x copied onto q (keeps -0.0), the reciprocal-refinement scheme of Markstein (IBM J. Res. Dev. 34(1), 1990).
 // Its agreement with the IEEE quotient is not assumed: the whole input domain
 // of this kernel (every finite fp16 row maximum times every fp16 x with
 // |x| <= max) is checked exhaustively on the CPU by the test suite.
@@ -51,10 +51,12 @@ __device__ __forceinline__ uint32_t e4m3_code(float q) {
   return (c | sign) & 0xFFu;
 }
 
+// The refinement yields +0 for x = -0 (fma(+0, y, -0) = +0); sa and y are
+// positive, so the quotient always carries the sign of x and copysign restores it.
 __device__ __forceinline__ float quotient(float x, float sa, float y) {
   const float q0 = x * y;
   const float r = __builtin_fmaf(-q0, sa, x);
-  return __builtin_fmaf(r, y, q0);
+  return __builtin_copysignf(__builtin_fmaf(r, y, q0), x);
 }
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {

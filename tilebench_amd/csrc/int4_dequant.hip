@@ -3,11 +3,12 @@
 // out[k, n] = fp16((q[k, n] - z[k/G, n]) * s[k/G, n]) with q, z int4 codes in
 // the N-packed, low-nibble-first layout (byte [k, j] = q[k,2j] | q[k,2j+1] << 4).
 //
-// Vector path: one thread owns 32 consecutive columns (one 16-byte packed load
-// per row) over ROWS consecutive rows of one group.  Its scales (64 B) and
-// zero-points (16 B) are loaded once and kept in registers as half2 pairs; each
-// row then costs one 16-byte load and four 16-byte stores, all coalesced
-// across the wavefront.  Codes become fp16 through the 0x6400 magic number
+// Vector path: a lane owns 8 consecutive columns (one packed dword per row)
+// over ROWS consecutive rows of one group; consecutive lanes own consecutive
+// column groups, so every wavefront-wide load (4 B per lane) and store (16 B
+// per lane, 8 fp16) covers one contiguous span of a row.  The lane's 8 scales
+// (16 B) and 8 zero-points (4 B) are loaded once per ROWS rows and kept in
+// registers as half2 pairs.  Codes become fp16 through the 0x6400 magic number
 // (1024 + q, exact), the zero-point subtraction is exact, and the single
 // rounding is the half2 multiply by the scale (RNE), so the result is
 // bit-identical to fp16(float(q - z) * float(s)).
@@ -30,55 +31,36 @@ __device__ __forceinline__ void unpack8(uint32_t w, f16x2 (&h)[4]) {
 }
 
 template <int ROWS>
-__global__ void __launch_bounds__(256) int4_dequant_vec(const u32x4* __restrict__ packed,
+__global__ void __launch_bounds__(256) int4_dequant_vec(const uint32_t* __restrict__ packed,
                                                         const u32x4* __restrict__ scales,
-                                                        const u32x4* __restrict__ zeros,
+                                                        const uint32_t* __restrict__ zeros,
                                                         u32x4* __restrict__ out, int64_t K, int64_t N,
                                                         int64_t group) {
-  const int64_t chunks = N >> 5;  // 32-column chunks per row
+  const int64_t cgs = N >> 3;  // 8-column groups per row
   const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t c = tid % chunks;
-  const int64_t r0 = (tid / chunks) * ROWS;
+  const int64_t c = tid % cgs;
+  const int64_t r0 = (tid / cgs) * ROWS;
   if (r0 >= K) return;
   const int64_t g = r0 / group;
 
-  // Zero-points of the 32 columns: 16 bytes -> 16 half2 of (1024 + z).
-  f16x2 zh[16];
-  {
-    const u32x4 zw = zeros[g * chunks + c];
+  uint32_t w[ROWS];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f16x2 t[4];
-      unpack8(zw[i], t);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) zh[4 * i + j] = t[j];
-    }
-  }
-  // Scales of the 32 columns: 64 bytes -> 16 half2.
-  f16x2 sh[16];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const u32x4 sw = scales[(g * chunks + c) * 4 + i];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) sh[4 * i + j] = as_h2(sw[j]);
-  }
+  for (int r = 0; r < ROWS; ++r) w[r] = __builtin_nontemporal_load(packed + (r0 + r) * cgs + c);
 
-  u32x4 w[ROWS];
+  f16x2 zh[4], sh[4];
+  unpack8(zeros[g * cgs + c], zh);
+  const u32x4 sw = scales[g * cgs + c];
 #pragma unroll
-  for (int r = 0; r < ROWS; ++r) w[r] = ld_nt(packed + (r0 + r) * chunks + c);
+  for (int j = 0; j < 4; ++j) sh[j] = as_h2(sw[j]);
 
 #pragma unroll
   for (int r = 0; r < ROWS; ++r) {
-    u32x4* dst = out + ((r0 + r) * chunks + c) * 4;
+    f16x2 h[4];
+    unpack8(w[r], h);
+    u32x4 o;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f16x2 h[4];
-      unpack8(w[r][i], h);
-      u32x4 o;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] = as_u32((h[j] - zh[4 * i + j]) * sh[4 * i + j]);
-      st_nt(dst + i, o);
-    }
+    for (int j = 0; j < 4; ++j) o[j] = as_u32((h[j] - zh[j]) * sh[j]);
+    st_nt(out + (r0 + r) * cgs + c, o);
   }
 }
 
@@ -112,16 +94,16 @@ extern "C" tb_status tb_int4_dequant(const uint8_t* packed, const uint16_t* scal
   TB_CHECK_ARG(N % 2 == 0, "tb_int4_dequant: N must be even (got %lld)", (long long)N);
   TB_CHECK_ARG(K % group == 0, "tb_int4_dequant: K=%lld is not a multiple of group=%lld", (long long)K,
                (long long)group);
-  constexpr int ROWS = 4;
-  const bool vec = (N % 32 == 0) && (group % ROWS == 0) && tb::aligned(packed, 16) && tb::aligned(scales, 16) &&
+  constexpr int ROWS = 8;
+  const bool vec = (N % 8 == 0) && (group % ROWS == 0) && tb::aligned(packed, 16) && tb::aligned(scales, 16) &&
                    tb::aligned(zeros, 16) && tb::aligned(out, 16);
   if (vec) {
-    const int64_t threads = (N / 32) * (K / ROWS);
+    const int64_t threads = (N / 8) * (K / ROWS);
     const int64_t blocks = (threads + 255) / 256;
     TB_CHECK_ARG(blocks < (1ll << 31), "tb_int4_dequant: problem too large");
     hipLaunchKernelGGL(tb::int4_dequant_vec<ROWS>, dim3((unsigned)blocks), dim3(256), 0, stream,
-                       reinterpret_cast<const tb::u32x4*>(packed), reinterpret_cast<const tb::u32x4*>(scales),
-                       reinterpret_cast<const tb::u32x4*>(zeros), reinterpret_cast<tb::u32x4*>(out), K, N, group);
+                       reinterpret_cast<const uint32_t*>(packed), reinterpret_cast<const tb::u32x4*>(scales),
+                       reinterpret_cast<const uint32_t*>(zeros), reinterpret_cast<tb::u32x4*>(out), K, N, group);
   } else {
     const int64_t blocks = (K * (N / 2) + 255) / 256;
     TB_CHECK_ARG(blocks < (1ll << 31), "tb_int4_dequant: problem too large");

@@ -63,6 +63,7 @@ __device__ __forceinline__ void store_weight(void* base, int64_t i, float w) {
 
 constexpr int kBlock = 256;
 constexpr int kPad = 4;  // LDS row padding (dwords) against bank conflicts
+constexpr int kBatch = 8;  // 16-byte loads in flight per thread while staging
 
 template <int DT, int V, int LPR, int KMAX>
 __global__ void __launch_bounds__(kBlock) gating_kernel(const void* __restrict__ logits, void* __restrict__ weights,
@@ -73,39 +74,46 @@ __global__ void __launch_bounds__(kBlock) gating_kernel(const void* __restrict__
   const int64_t row0 = (int64_t)blockIdx.x * ROWS;
   const int nrows = (int)((M - row0) < ROWS ? (M - row0) : ROWS);
 
-  // Stage the block's rows (contiguous in HBM) as keys.
+  // Stage the block's rows (contiguous in HBM) as keys.  Loads are issued in
+  // batches of kBatch independent 16-byte loads per thread before any of them
+  // is consumed, so one HBM round trip covers a batch.
   {
     const int64_t base = row0 * E;
     const int total = nrows * E;
-    if constexpr (DT == 0) {
-      if ((E & 3) == 0) {
-        const u32x4* src = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint32_t*>(logits) + base);
-        for (int v = threadIdx.x; v < (total >> 2); v += kBlock) {
-          const u32x4 x = src[v];
-          const int e = v * 4, r = e / E, c = e - r * E;
+    constexpr int EPV = DT == 0 ? 4 : 8;  // elements per 16-byte vector
+    if ((E % EPV) == 0) {
+      const u32x4* src = reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(logits) +
+                                                        base * (DT == 0 ? 4 : 2));
+      const int nvec = total / EPV;
+      for (int v0 = threadIdx.x; v0 < nvec; v0 += kBlock * kBatch) {
+        u32x4 x[kBatch];
 #pragma unroll
-          for (int t = 0; t < 4; ++t) lds[r * stride + c + t] = key_of_bits(x[t]);
+        for (int b = 0; b < kBatch; ++b) {
+          const int v = v0 + b * kBlock;
+          if (v < nvec) x[b] = src[v];
         }
-      } else {
-        for (int e = threadIdx.x; e < total; e += kBlock) lds[(e / E) * stride + e % E] = load_key<DT>(logits, base + e);
-      }
-    } else {
-      if ((E & 7) == 0) {
-        const u32x4* src = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(logits) + base);
-        for (int v = threadIdx.x; v < (total >> 3); v += kBlock) {
-          const u32x4 x = src[v];
-          const int e = v * 8, r = e / E, c = e - r * E;
 #pragma unroll
-          for (int t = 0; t < 8; ++t) {
-            const uint32_t h = (x[t >> 1] >> (16 * (t & 1))) & 0xFFFFu;
-            const uint32_t fb = DT == 1 ? __builtin_bit_cast(uint32_t, (float)__builtin_bit_cast(_Float16, (uint16_t)h))
-                                        : (h << 16);
-            lds[r * stride + c + t] = key_of_bits(fb);
+        for (int b = 0; b < kBatch; ++b) {
+          const int v = v0 + b * kBlock;
+          if (v < nvec) {
+            const int e = v * EPV, r = e / E, c = e - r * E;
+#pragma unroll
+            for (int t = 0; t < EPV; ++t) {
+              uint32_t fb;
+              if constexpr (DT == 0) {
+                fb = x[b][t];
+              } else {
+                const uint32_t h = (x[b][t >> 1] >> (16 * (t & 1))) & 0xFFFFu;
+                fb = DT == 1 ? __builtin_bit_cast(uint32_t, (float)__builtin_bit_cast(_Float16, (uint16_t)h))
+                             : (h << 16);
+              }
+              lds[r * stride + c + t] = key_of_bits(fb);
+            }
           }
         }
-      } else {
-        for (int e = threadIdx.x; e < total; e += kBlock) lds[(e / E) * stride + e % E] = load_key<DT>(logits, base + e);
       }
+    } else {
+      for (int e = threadIdx.x; e < total; e += kBlock) lds[(e / E) * stride + e % E] = load_key<DT>(logits, base + e);
     }
   }
   __syncthreads();

@@ -35,6 +35,8 @@ SIGNATURES: dict[str, list] = {
     "tb_int4_dequant": [_c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p],
     "tb_moe_topk_gating": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p],
     "tb_fp8_act_quant": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_p],
+    "tb_w4a16_gemm": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p],
+    "tb_w4a16_workspace_size": [_c_i64, _c_i64, _c_i64, _c_i64, ctypes.POINTER(_c_i64)],
     "tb_l2_flush": [_c_p, _c_i64, _c_u32, _c_p],
     "tb_probe_copy": [_c_p, _c_p, _c_i64, _c_p],
 }
@@ -120,3 +122,30 @@ def call(name: str, *args) -> None:
 def ptr(t) -> int:
     """data_ptr of a tensor (0 for None)."""
     return 0 if t is None else t.data_ptr()
+
+
+_workspaces: dict = {}
+
+
+def workspace(nbytes: int, device, stream: int):
+    """A zero-filled device workspace of at least `nbytes`, cached per device.
+
+    Kernels that use one restore every counter they touch to zero, so the
+    buffer is zero-filled only when it is first allocated (outside any graph
+    capture: the engine and the bench always run a call eagerly first).  One
+    buffer per device serves calls issued in order on one stream (graph
+    replays included); calls running concurrently on several streams of one
+    device would race on it and are not supported."""
+    import torch
+
+    del stream  # calls are serialised on one stream; see the docstring
+    if nbytes <= 0:
+        return None
+    key = str(device)
+    buf = _workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("workspace must be allocated before graph capture (run the op once eagerly)")
+        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = buf
+    return buf
