@@ -206,3 +206,23 @@ def test_w4a16_decode_repeat_calls_reuse_workspace(gpu):
         assert diff.numel() == 0, (f"call {i}: {diff.shape[0]} outputs differ from call 0, first "
                                    f"{diff[:4].tolist()}: {[float(o[m, n]) for m, n in diff[:4].tolist()]} vs "
                                    f"{[float(first[m, n]) for m, n in diff[:4].tolist()]}")
+
+
+@pytest.mark.parametrize("M", [16, 3])
+def test_w4a16_decode_alternating_inputs(gpu, M):
+    """Back-to-back decode calls on two different inputs of one shape: every
+    result matches its own oracle (stale split-K partials would mix them)."""
+    from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip
+
+    _say("w4a16_gemm decode alternating", M)
+    K, N, G = 2048, 4096, 128
+    sets = [T.generate_w4a16_gemm_inputs(M, K, N, G, seed=s, device="cpu") for s in (21, 22)]
+    refs = [oracle.w4a16_gemm(A.numpy(), p.numpy(), s.numpy(), z.numpy(), G) for A, p, s, z, G in sets]
+    dev = [tuple(t.to(gpu) if isinstance(t, torch.Tensor) else t for t in x) for x in sets]
+    outs = [impl_hip.run(*dev[i % 2]) for i in range(6)]
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs):
+        np.testing.assert_allclose(o.cpu().numpy().astype(np.float32), refs[i % 2].astype(np.float32),
+                                   atol=1e-2, rtol=1e-2, err_msg=f"call {i}")
+    for i in range(2, 6):
+        assert torch.equal(outs[i], outs[i % 2]), f"call {i} differs from call {i % 2}"

@@ -246,6 +246,8 @@ typedef float f32x4d __attribute__((ext_vector_type(4)));
 struct DecUnit {
   uint32_t w[8];
   u32x4 a;
+  u32x4 s;
+  uint32_t z;
 };
 
 __global__ void __launch_bounds__(DEC_THREADS)
@@ -278,10 +280,11 @@ __global__ void __launch_bounds__(DEC_THREADS)
       d.w[r] = col_ok ? __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(W + (int64_t)(k + r) * half_n + (n >> 1)))
                       : 0u;
     d.a = arow < M ? *reinterpret_cast<const u32x4*>(A + (int64_t)arow * K + k) : u32x4{0u, 0u, 0u, 0u};
+    const int g = (u * DEC_UNIT) / group;
+    d.s = col_ok ? *reinterpret_cast<const u32x4*>(S + (int64_t)g * N + n) : u32x4{0u, 0u, 0u, 0u};
+    d.z = col_ok ? *reinterpret_cast<const uint32_t*>(Z + (int64_t)g * half_n + (n >> 1)) : 0u;
   };
 
-  int g_cached = -1;
-  f16x2 zh[4], sh[4];
   for (int u0 = u_begin + wave; u0 < u_end; u0 += 4 * DEC_PREFETCH) {
     DecUnit d[DEC_PREFETCH];
 #pragma unroll
@@ -291,15 +294,10 @@ __global__ void __launch_bounds__(DEC_THREADS)
     for (int p = 0; p < DEC_PREFETCH; ++p) {
       const int u = u0 + 4 * p;
       if (u >= u_end) break;
-      const int g = (u * DEC_UNIT) / group;
-      if (g != g_cached) {
-        g_cached = g;
-        const u32x4 sv = col_ok ? *reinterpret_cast<const u32x4*>(S + (int64_t)g * N + n) : u32x4{0u, 0u, 0u, 0u};
-        const uint32_t zv = col_ok ? *reinterpret_cast<const uint32_t*>(Z + (int64_t)g * half_n + (n >> 1)) : 0u;
-        unpack8(zv, zh);
+      f16x2 zh[4], sh[4];
+      unpack8(d[p].z, zh);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sh[j] = as_h2(sv[j]);
-      }
+      for (int j = 0; j < 4; ++j) sh[j] = as_h2(d[p].s[j]);
       uint32_t dq[8][4];
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
@@ -340,21 +338,26 @@ __global__ void __launch_bounds__(DEC_THREADS)
     }
     return;
   }
-  // Serial split-K across the slab's blocks.
+  // Serial split-K across the slab's blocks.  Every access to the partials and
+  // the counters is a device-scope atomic (coherent across the XCDs' L2s), so
+  // no cache-wide fence is needed: each thread waits until its partial stores
+  // are acknowledged (s_waitcnt 0) before the block's arrival is counted, and
+  // the last block reads the partials with device-scope loads.  (A release /
+  // acquire fence would write back and invalidate the whole L2 of the XCD in
+  // every block.)
   float* mine = partials + ((int64_t)split * M) * N;
   for (int i = threadIdx.x; i < M * DEC_COLS; i += DEC_THREADS) {
     const int m = i / DEC_COLS, cc = i % DEC_COLS;
     if (cc < ncols) __hip_atomic_store(&mine[(int64_t)m * N + n0 + cc], red[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  __threadfence();
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(&counters[slab], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const int prev = __hip_atomic_fetch_add(&counters[slab], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last_flag = (prev == splits - 1);
   }
   __syncthreads();
   if (!last_flag) return;
-  __threadfence();
   for (int i = threadIdx.x; i < M * DEC_COLS; i += DEC_THREADS) {
     const int m = i / DEC_COLS, cc = i % DEC_COLS;
     if (cc >= ncols) continue;
