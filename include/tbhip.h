@@ -128,6 +128,16 @@ tb_status tb_l2_flush(void* buf, int64_t bytes, uint32_t pattern, hipStream_t st
  */
 tb_status tb_probe_copy(const void* src, void* dst, int64_t bytes, hipStream_t stream);
 
+/*
+ * Calibration probe: `blocks` x 256 threads, each wavefront issuing
+ * 8 * iters independent MFMAs (kind 0: v_mfma_f32_32x32x16_f16, 32768 flop
+ * each; kind 1: v_mfma_f32_32x32x64_f8f6f4 on e4m3, 131072 flop each), then
+ * one float per thread into out[blocks * 256].  The measured MFMA peak is
+ * taken from it.
+ * Replaces: tilebench/llm/v2/calibration/gpu_probes.py:225 probe_gemm().
+ */
+tb_status tb_probe_mfma(int kind, int64_t blocks, int64_t iters, float* out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -38,6 +38,53 @@ __global__ void __launch_bounds__(256) copy_kernel(const u32x4* __restrict__ src
   for (; i < n16; i += stride) st_nt(dst + i, ld_nt(src + i));
 }
 
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+// MFMA throughput probe: every wavefront keeps 8 independent 32x32 accumulators
+// busy for `iters` rounds, so the matrix pipe never waits on a dependency; the
+// accumulators are reduced to one store per lane so nothing is dead code.
+// kind 0: v_mfma_f32_32x32x16_f16 (32768 flop), kind 1: v_mfma_f32_32x32x64_f8f6f4
+// with e4m3 operands (131072 flop).
+template <int KIND>
+__global__ void __launch_bounds__(256) mfma_probe_kernel(float* __restrict__ out, int iters, float seed) {
+  f32x16 acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = f32x16{};
+  const int lane = threadIdx.x;
+  if constexpr (KIND == 0) {
+    h8 a, b;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      a[i] = (_Float16)(seed * (lane + i));
+      b[i] = (_Float16)(seed * (lane - i));
+    }
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[i], 0, 0, 0);
+    }
+  } else {
+    i32x8 a, b;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      a[i] = (int)(0x38383838u + lane + i);
+      b[i] = (int)(0x30303030u + lane - i);
+    }
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        acc[i] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc[i], 0, 0, 0, 0, 0, 0);
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s += acc[i][e];
+  out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
 static int grid_for(int64_t n16) {
   // 256 CUs x 8 resident 256-thread blocks; never more blocks than granules.
   int64_t blocks = (n16 + 255) / 256;
@@ -60,6 +107,17 @@ tb_status tb_l2_flush(void* buf, int64_t bytes, uint32_t pattern, hipStream_t st
   hipLaunchKernelGGL(tb::fill_kernel, dim3(tb::grid_for(n16)), dim3(256), 0, stream,
                      reinterpret_cast<tb::u32x4*>(buf), n16, pattern);
   return tb::launch_status("tb_l2_flush");
+}
+
+tb_status tb_probe_mfma(int kind, int64_t blocks, int64_t iters, float* out, hipStream_t stream) {
+  TB_CHECK_ARG(out != nullptr && blocks > 0 && blocks < (1 << 24) && iters > 0 && iters < (1 << 30),
+               "tb_probe_mfma: bad arguments");
+  TB_CHECK_ARG(kind == 0 || kind == 1, "tb_probe_mfma: kind must be 0 (fp16) or 1 (fp8)");
+  if (kind == 0)
+    hipLaunchKernelGGL(tb::mfma_probe_kernel<0>, dim3((unsigned)blocks), dim3(256), 0, stream, out, (int)iters, 1e-3f);
+  else
+    hipLaunchKernelGGL(tb::mfma_probe_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, stream, out, (int)iters, 1e-3f);
+  return tb::launch_status("tb_probe_mfma");
 }
 
 tb_status tb_probe_copy(const void* src, void* dst, int64_t bytes, hipStream_t stream) {
