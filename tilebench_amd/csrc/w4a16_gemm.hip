@@ -3,26 +3,31 @@
 // A is fp16 row-major; W is int4 in the N-packed, low-nibble-first layout with
 // group-wise fp16 scales and int4 zero-points along K (see include/tbhip.h).
 //
-// Prefill kernel (MFMA-bound for large M): 256 x 256 output tile per
-// 256-thread block, four wavefronts in a 2 x 2 arrangement each owning a
-// 128 x 128 sub-tile (16 v_mfma_f32_32x32x16_f16 accumulators = 256 fp32 per
-// lane), K advanced 64 at a time through a two-stage LDS pipeline:
+// Prefill kernel (MFMA-bound for large M): one 256 x 256 output tile per
+// 512-thread block, eight wavefronts (two per SIMD) each owning a 128 x 64
+// sub-tile (8 v_mfma_f32_32x32x16_f16 accumulators = 128 fp32 per lane), K
+// advanced 64 at a time:
 //
-//   global -> registers : the A tile (256 x 64 fp16, eight 16-byte loads per
-//                         thread) and the packed W tile (64 x 256 int4, eight
-//                         4-byte row loads per thread: 8 rows x 8 columns) for
-//                         step i+1 are issued before the MFMAs of step i;
-//   dequantise          : each thread turns its 8 x 8 int4 block into fp16 once
-//                         per block ((1024 + q) via the 0x6400 magic number,
-//                         exact zero-point subtraction, one RNE multiply by the
-//                         scale: bit-identical to the standalone dequantiser) and
-//                         transposes it with byte permutes so that every column
-//                         holds 8 consecutive k;
-//   LDS                 : A as [256][64] and W^T as [256][64] fp16, 16-byte chunks
-//                         XOR-swizzled by (row & 7) so the fragment reads of a
-//                         wavefront spread over all banks;
-//   MFMA                : per k16 step each wavefront reads 4 A and 4 B fragments
-//                         (one ds_read_b128 per lane each) and issues 16 MFMAs.
+//   A     : streamed HBM -> LDS by the buffer unit (buffer_load ... lds, no
+//           registers), three LDS stages, issued two steps ahead;
+//   W     : packed int4 tile prefetched two steps ahead into registers (each
+//           thread: 4 rows x 8 columns + its scales and zero-points), then
+//           dequantised once per block ((1024 + q) via the 0x6400 magic number,
+//           exact zero-point subtraction, one RNE multiply by the scale:
+//           bit-identical to the standalone dequantiser), transposed with byte
+//           permutes so each column holds consecutive k, and written to one of
+//           two LDS stages as W^T;
+//   LDS   : rows of 64 halfs in 16-byte chunks, chunk c of row r at slot
+//           c ^ ((r ^ (r >> 3)) & 7): the fragment reads (8 consecutive rows)
+//           and the W^T writes (rows 8 apart) are both free of bank conflicts;
+//   MFMA  : per k16 step a wavefront reads 4 A and 2 B fragments (one
+//           ds_read_b128 each) and issues 8 MFMAs;
+//   order : every K step is split in two halves by a barrier.  The wavefronts
+//           of rows 0-127 run their MFMAs in the first half and dequantise in
+//           the second, those of rows 128-255 the other way round, so each
+//           SIMD always has one wavefront feeding its matrix pipe while the
+//           other keeps the vector ALU busy.
+//   output: the fp16 tile is staged in LDS and written with 16-byte row stores.
 //
 // Tiles are numbered XCD-aware: consecutive hardware block ids land on
 // different XCDs, so block ids are first regrouped so that each XCD owns a
@@ -40,12 +45,8 @@ namespace w4a16 {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 256, BN = 256, BK = 64, THREADS = 256;
+constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int GROUP_M = 4;  // tile rows per ordering group
-constexpr int STAGE_HALFS = (BM + BN) * BK;
-constexpr size_t LDS_BYTES = 2 * STAGE_HALFS * sizeof(_Float16);  // 128 KiB
-
-__device__ __forceinline__ int swz(int row, int chunk) { return (row * 8 + (chunk ^ (row & 7))) * 8; }
 
 // (1024 + q) half2 pairs of one packed dword: columns (0,1), (2,3), (4,5), (6,7).
 __device__ __forceinline__ void unpack8(uint32_t w, f16x2 (&h)[4]) {
@@ -76,148 +77,228 @@ __device__ __forceinline__ Tile tile_of_block(int tiles_m, int tiles_n) {
   return t;
 }
 
-struct Prefetch {
-  u32x4 a[8];
-  uint32_t w[8];
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+constexpr uint32_t RSRC_DW3 = 0x00020000u;
+constexpr uint32_t OOB = 0x80000000u;
+constexpr int T4 = 512;
+constexpr int A_STAGE = BM * BK;  // halfs
+constexpr int B_STAGE = BN * BK;  // halfs
+constexpr int A_STAGES = 3, B_STAGES = 2;
+constexpr size_t LDS4_BYTES = (size_t)(A_STAGES * A_STAGE + B_STAGES * B_STAGE) * 2;  // 160 KiB
+constexpr int C_STRIDE = BN + 8;  // halfs per row of the staged output tile (16 B pad)
+
+__device__ __forceinline__ int swz2(int row, int chunk) { return (row * 8 + (chunk ^ ((row ^ (row >> 3)) & 7))) * 8; }
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, (int)RSRC_DW3);
+}
+
+struct WRegs4 {
+  uint32_t w[4];
   u32x4 s;
   uint32_t z;
 };
 
-__device__ __forceinline__ void load_tile(Prefetch& p, const _Float16* __restrict__ A, const uint8_t* __restrict__ W,
-                                          const _Float16* __restrict__ S, const uint8_t* __restrict__ Z, int M,
-                                          int N, int K, int group, int m0, int n0, int k0) {
-  const int t = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int id = i * THREADS + t, row = id >> 3, c = id & 7;
-    const int m = m0 + row;
-    if (m < M) p.a[i] = *reinterpret_cast<const u32x4*>(A + (int64_t)m * K + k0 + c * 8);
-    else p.a[i] = u32x4{0u, 0u, 0u, 0u};
-  }
-  const int cg = t & 31, kg = t >> 5;
-  const int n = n0 + cg * 8;
-  if (n < N) {
-    const int64_t half_n = N >> 1;
-#pragma unroll
-    for (int r = 0; r < 8; ++r)
-      p.w[r] = *reinterpret_cast<const uint32_t*>(W + (int64_t)(k0 + kg * 8 + r) * half_n + (n >> 1));
-    const int g = k0 / group;
-    p.s = *reinterpret_cast<const u32x4*>(S + (int64_t)g * N + n);
-    p.z = *reinterpret_cast<const uint32_t*>(Z + (int64_t)g * half_n + (n >> 1));
-  } else {
-#pragma unroll
-    for (int r = 0; r < 8; ++r) p.w[r] = 0u;
-    p.s = u32x4{0u, 0u, 0u, 0u};
-    p.z = 0u;
-  }
-}
-
-__device__ __forceinline__ void store_tile(const Prefetch& p, _Float16* __restrict__ lds) {
-  const int t = threadIdx.x;
-  _Float16* la = lds;
-  _Float16* lb = lds + BM * BK;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int id = i * THREADS + t, row = id >> 3, c = id & 7;
-    *reinterpret_cast<u32x4*>(la + swz(row, c)) = p.a[i];
-  }
-  // Dequantise the 8 x 8 block: rows kg*8 + r, columns cg*8 + 0..7.
-  const int cg = t & 31, kg = t >> 5;
-  f16x2 zh[4], sh[4];
-  unpack8(p.z, zh);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) sh[j] = as_h2(p.s[j]);
-  uint32_t d[8][4];  // d[r][j] = half2(col 2j, col 2j+1) of row r
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    f16x2 h[4];
-    unpack8(p.w[r], h);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) d[r][j] = as_u32((h[j] - zh[j]) * sh[j]);
-  }
-  // 2 x 2 half transposes: column 2j+e gets rows (2p, 2p+1) in one dword.
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const uint32_t sel = e ? 0x07060302u : 0x05040100u;
-      u32x4 col;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) col[q] = perm(d[2 * q + 1][j], d[2 * q][j], sel);
-      const int nrow = cg * 8 + 2 * j + e;
-      *reinterpret_cast<u32x4*>(lb + swz(nrow, kg)) = col;
-    }
-  }
-}
-
-__global__ void __launch_bounds__(THREADS, 1)
+__global__ void __launch_bounds__(T4, 1)
     w4a16_prefill(const _Float16* __restrict__ A, const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
                   const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int M, int N, int K, int group,
                   int tiles_m, int tiles_n) {
   extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+  _Float16* const lds_a = lds;
+  _Float16* const lds_b = lds + A_STAGES * A_STAGE;
   const Tile tile = tile_of_block(tiles_m, tiles_n);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
 
-  f32x16 acc[4][4];
+  const rsrc_t rw = make_rsrc(W, (uint32_t)K * (uint32_t)(N / 2));
+  const rsrc_t rs = make_rsrc(S, (uint32_t)(K / group) * (uint32_t)N * 2u);
+  const rsrc_t rz = make_rsrc(Z, (uint32_t)(K / group) * (uint32_t)(N / 2));
+  i32x4 ra4;
+  {
+    const uint64_t base = (uint64_t)(uintptr_t)A;
+    ra4[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)base);
+    ra4[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(base >> 32) & 0xFFFF);
+    ra4[2] = __builtin_amdgcn_readfirstlane((int)((uint32_t)M * (uint32_t)K * 2u));
+    ra4[3] = (int)RSRC_DW3;
+  }
+
+  // A DMA: 32 instructions of 1 KiB (8 rows) per tile, 4 per wavefront.
+  uint32_t a_off[4];
+  {
+    const int lr = lane >> 3;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = (wave * 4 + i) * 8 + lr;
+      const int lc = (lane & 7) ^ ((row ^ (row >> 3)) & 7);
+      const int m = tile.m0 + row;
+      a_off[i] = m < M ? ((uint32_t)m * (uint32_t)K + (uint32_t)lc * 8u) * 2u : OOB;
+    }
+  }
+  const uint32_t a_lds0 = (uint32_t)__builtin_amdgcn_readfirstlane(
+      (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_a) + (uint32_t)(wave * 4 * 1024);
+
+  // W: thread owns rows kq*4 .. kq*4+3 of the 64-row step, columns cg*8 .. +7.
+  const int cg = t & 31, kq = t >> 5;
+  const int n = tile.n0 + cg * 8;
+  const uint32_t w_row = (uint32_t)(N / 2);
+  const uint32_t w_off = n < N ? (uint32_t)(kq * 4) * w_row + (uint32_t)(n / 2) : OOB;
+  const uint32_t s_off = n < N ? (uint32_t)n * 2u : OOB;
+  const uint32_t z_off = n < N ? (uint32_t)(n / 2) : OOB;
+  int b_st[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) b_st[c] = swz2(cg * 8 + c, kq >> 1) + (kq & 1) * 4;
+
+  // fragment read offsets (halfs) for k16 step ks and row parity of the fragment index
+  const int fa_base = (wm * 128 + (lane & 31)) * 64;
+  const int fb_base = (wn * 64 + (lane & 31)) * 64;
+  int fx[4][2];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int ip = 0; ip < 2; ++ip) {
+      const int r = ip * 32 + (lane & 31);
+      fx[ks][ip] = ((ks * 2 + (lane >> 5)) ^ ((r ^ (r >> 3)) & 7)) * 8;
+    }
+
+  auto issue_a = [&](int kt) {
+    const uint32_t st = a_lds0 + (uint32_t)((kt % A_STAGES) * A_STAGE * 2);
+    const uint32_t soff = (uint32_t)(kt * BK) * 2u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                   :
+                   : "s"(__builtin_amdgcn_readfirstlane((int)(st + (uint32_t)(i * 1024)))), "v"(a_off[i]), "s"(ra4),
+                     "s"(__builtin_amdgcn_readfirstlane((int)soff))
+                   : "memory", "m0");
+    }
+  };
+  auto issue_w = [&](WRegs4& r, int kt) {
+    const uint32_t k0 = (uint32_t)(kt * BK);
+    const uint32_t kw = k0 * w_row;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) r.w[q] = __builtin_amdgcn_raw_buffer_load_b32(rw, w_off + q * w_row, kw, 0);
+    const uint32_t g = k0 / (uint32_t)group;
+    r.s = __builtin_amdgcn_raw_buffer_load_b128(rs, s_off, g * (uint32_t)N * 2u, 0);
+    r.z = __builtin_amdgcn_raw_buffer_load_b32(rz, z_off, g * w_row, 0);
+  };
+  auto dequant_store = [&](const WRegs4& r, _Float16* st) {
+    f16x2 zh[4], sh[4];
+    unpack8(r.z, zh);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sh[j] = as_h2(r.s[j]);
+    uint32_t d[4][4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      f16x2 h[4];
+      unpack8(r.w[q], h);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) d[q][j] = as_u32((h[j] - zh[j]) * sh[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const uint32_t sel = e ? 0x07060302u : 0x05040100u;
+        u32x2v col;
+        col[0] = perm(d[1][j], d[0][j], sel);
+        col[1] = perm(d[3][j], d[2][j], sel);
+        *reinterpret_cast<u32x2v*>(st + b_st[2 * j + e]) = col;
+      }
+  };
+
+  f32x16 acc[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
-  Prefetch pf;
-  load_tile(pf, A, W, S, Z, M, N, K, group, tile.m0, tile.n0, 0);
-  store_tile(pf, lds);
-  __syncthreads();
-
-  const int nk = K / BK;
-  for (int it = 0; it < nk; ++it) {
-    const bool more = it + 1 < nk;
-    if (more) load_tile(pf, A, W, S, Z, M, N, K, group, tile.m0, tile.n0, (it + 1) * BK);
-    const _Float16* la = lds + (it & 1) * STAGE_HALFS;
-    const _Float16* lb = la + BM * BK;
+  auto mfma_stage = [&](const _Float16* sa, const _Float16* sb) {
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int chunk = ks * 2 + (lane >> 5);
-      h8 af[4], bf[4];
+    for (int ks = 0; ks < 4; ++ks) {
+      h8 fa[4], fb[2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = wm * 128 + i * 32 + (lane & 31);
-        af[i] = *reinterpret_cast<const h8*>(la + swz(row, chunk));
-      }
+      for (int i = 0; i < 4; ++i) fa[i] = *reinterpret_cast<const h8*>(sa + fa_base + i * 32 * 64 + fx[ks][i & 1]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int col = wn * 128 + j * 32 + (lane & 31);
-        bf[j] = *reinterpret_cast<const h8*>(lb + swz(col, chunk));
-      }
+      for (int j = 0; j < 2; ++j) fb[j] = *reinterpret_cast<const h8*>(sb + fb_base + j * 32 * 64 + fx[ks][j & 1]);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
-    if (more) store_tile(pf, lds + ((it + 1) & 1) * STAGE_HALFS);
-    __syncthreads();
-  }
+  };
 
-  // Epilogue: accumulator element e of fragment (i, j) is row
-  // i*32 + (e/4)*8 + (lane/32)*4 + e%4, column j*32 + lane%32 of the wave tile.
-  const int col_base = tile.n0 + wn * 128 + (lane & 31);
+  constexpr int WAIT_VM10 = (10 & 15) | (7 << 4) | (15 << 8);
+  constexpr int WAIT_VM0 = 0 | (7 << 4) | (15 << 8);
+  const int nk = K / BK;
+  WRegs4 w0, w1;
+  issue_a(0);
+  if (nk > 1) issue_a(1);
+  issue_w(w0, 0);
+  if (nk > 1) issue_w(w1, 1);
+  dequant_store(w0, lds_b);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  auto step = [&](int kt, WRegs4& nxt, WRegs4& fill) {
+    const bool more = kt + 2 < nk;
+    if (more) {
+      issue_a(kt + 2);
+      issue_w(fill, kt + 2);
+    }
+    // Two half-steps separated by a barrier: wave group 0 runs its MFMAs while
+    // group 1 dequantises, then the roles swap, so the MFMA pipe of every SIMD
+    // always has one wavefront feeding it.
+    if (wm == 1) {
+      if (kt + 1 < nk) dequant_store(nxt, lds_b + ((kt + 1) & 1) * B_STAGE);
+      __builtin_amdgcn_s_barrier();
+      mfma_stage(lds_a + (kt % A_STAGES) * A_STAGE, lds_b + (kt & 1) * B_STAGE);
+    } else {
+      mfma_stage(lds_a + (kt % A_STAGES) * A_STAGE, lds_b + (kt & 1) * B_STAGE);
+      __builtin_amdgcn_s_barrier();
+      if (kt + 1 < nk) dequant_store(nxt, lds_b + ((kt + 1) & 1) * B_STAGE);
+    }
+    // A tile kt+1 (DMA issued one step earlier) must have landed; the 10 loads
+    // issued in this step (4 DMA + 6 W) may stay in flight.
+    if (more) __builtin_amdgcn_s_waitcnt(WAIT_VM10);
+    else __builtin_amdgcn_s_waitcnt(WAIT_VM0);
+    __syncthreads();
+  };
+  int kt = 0;
+  for (; kt + 1 < nk; kt += 2) {
+    step(kt, w1, w0);
+    step(kt + 1, w0, w1);
+  }
+  if (kt < nk) step(kt, w1, w0);
+
+  // Epilogue: stage the fp16 tile in LDS, then store 16-byte row chunks.
+  // Accumulator element e of fragment (i, j) is row i*32 + (e/4)*8 + (lane/32)*4 + e%4,
+  // column j*32 + lane%32 of the wave tile.
+  _Float16* ct = lds;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int m = tile.m0 + wm * 128 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-      if (m < M) {
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int n = col_base + j * 32;
-          if (n < N) Y[(int64_t)m * N + n] = (_Float16)acc[i][j][e];
-        }
+      for (int e = 0; e < 16; ++e) {
+        const int row = wm * 128 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+        const int col = wn * 64 + j * 32 + (lane & 31);
+        ct[row * C_STRIDE + col] = (_Float16)acc[i][j][e];
       }
+  __syncthreads();
+  const int rows = min(BM, M - tile.m0);
+  const int cols = min(BN, N - tile.n0);
+#pragma unroll 4
+  for (int idx = t; idx < BM * (BN / 8); idx += T4) {
+    const int row = idx >> 5, ch = idx & 31;
+    if (row < rows && ch * 8 < cols) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(ct + row * C_STRIDE + ch * 8);
+      *reinterpret_cast<u32x4*>(Y + (int64_t)(tile.m0 + row) * N + tile.n0 + ch * 8) = v;
     }
   }
 }
-
 
 // ---------------------------------------------------------------------------
 // Decode kernel (M <= 16, HBM-bound on the weights).  A block owns a 128-column
@@ -438,14 +519,14 @@ extern "C" tb_status tb_w4a16_gemm(const uint16_t* A, const uint8_t* W, const ui
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a16_prefill), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)LDS_BYTES) != hipSuccess) {
-      tb::set_error("tb_w4a16_gemm: cannot reserve %zu bytes of LDS", LDS_BYTES);
+                            (int)LDS4_BYTES) != hipSuccess) {
+      tb::set_error("tb_w4a16_gemm: cannot reserve %zu bytes of LDS", LDS4_BYTES);
       return TB_E_HIP;
     }
     attr_set = true;
   }
   const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
-  hipLaunchKernelGGL(w4a16_prefill, dim3(tiles_m * tiles_n), dim3(THREADS), LDS_BYTES, stream,
+  hipLaunchKernelGGL(w4a16_prefill, dim3(tiles_m * tiles_n), dim3(T4), LDS4_BYTES, stream,
                      reinterpret_cast<const _Float16*>(A), W, reinterpret_cast<const _Float16*>(scales), zeros,
                      reinterpret_cast<_Float16*>(Y), (int)M, (int)N, (int)K, (int)group, tiles_m, tiles_n);
   return tb::launch_status("tb_w4a16_gemm");
