@@ -1,0 +1,332 @@
+"""Pins for the CPU oracle (no GPU).
+
+Each oracle function is checked against something that does not restate its
+own formula: the reference's worked examples (tilebench/problems/*.md), torch's
+CPU casts (the library the reference's own impl_torch relies on), exact rational
+arithmetic, brute force over tiny inputs, and algebraic invariants.
+"""
+import itertools
+import math
+import os
+import shutil
+import struct
+import subprocess
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def f16_rne(x: float) -> np.uint16:
+    """Round a Python float (exact in binary64) to fp16 bits with struct's
+    round-half-even packing: an implementation independent of numpy's cast.
+    Magnitudes from 65520 up round to infinity (struct refuses to pack them)."""
+    if x == 0:
+        return np.uint16(0x8000 if math.copysign(1.0, x) < 0 else 0)
+    if abs(x) >= 65520.0:
+        return np.uint16(0xFC00 if x < 0 else 0x7C00)
+    return np.frombuffer(struct.pack("<e", x), dtype=np.uint16)[0]
+
+
+# ----------------------------------------------------------------------------- int4 packing
+
+
+def test_pack_known_answer():
+    # byte 0x21 holds column 2j = 1 (low nibble) and column 2j+1 = 2 (high nibble)
+    assert oracle.unpack_int4(np.array([[0x21, 0xF0]], np.uint8)).tolist() == [[1, 2, 0, 15]]
+    assert oracle.pack_int4(np.array([[1, 2, 0, 15]], np.uint8)).tolist() == [[0x21, 0xF0]]
+
+
+def test_pack_roundtrip_and_validation():
+    q = np.random.default_rng(0).integers(0, 16, size=(7, 10), dtype=np.uint8)
+    assert np.array_equal(oracle.unpack_int4(oracle.pack_int4(q)), q)
+    with pytest.raises(ValueError):
+        oracle.pack_int4(np.array([[16, 0]], np.uint8))
+    with pytest.raises(ValueError):
+        oracle.pack_int4(np.zeros((1, 3), np.uint8))
+
+
+# ----------------------------------------------------------------------------- int4 dequant
+
+
+def test_dequant_reference_worked_example():
+    """tilebench/problems/weight_dequant_current.md:17-45 (M=N=4, T=2) recast as
+    int4 codes with zero-points 0 and per-(group, column) scales: the expected
+    output is the reference's."""
+    X = np.array([[10, 10, 5, 5], [10, 10, 5, 5], [2, 2, 8, 8], [2, 2, 8, 8]], np.uint8)
+    S = np.array([[0.5, 2.0], [4.0, 0.25]])
+    scales = np.repeat(S, 2, axis=1).astype(np.float16)            # s[g, n] = S[g, n // T]
+    out = oracle.int4_dequant(oracle.pack_int4(X), scales, oracle.pack_int4(np.zeros((2, 4), np.uint8)), 2)
+    expected = [[5, 5, 10, 10], [5, 5, 10, 10], [8, 8, 2, 2], [8, 8, 2, 2]]
+    assert out.astype(np.float64).tolist() == expected
+
+
+def test_dequant_exhaustive_codes_exact_rationals():
+    """All 256 (q, z) pairs against 64 fp16 scales spanning every magnitude band
+    and both signs: (q - z) * s computed exactly as a Fraction, rounded by struct."""
+    rng = np.random.default_rng(1)
+    sbits = np.concatenate([rng.integers(1, 0x7C00, 48, dtype=np.uint16), np.array([1, 0x3FF, 0x400, 0x7BFF], np.uint16)])
+    sbits = np.concatenate([sbits, sbits[:12] | 0x8000])
+    scales_1d = sbits.view(np.float16)
+    G = 16
+    K = 16 * G                          # group g: rows q = 0..15
+    N = 16 * len(scales_1d)              # column n: z = n % 16, scale index n // 16
+    q = np.tile(np.arange(16, dtype=np.uint8)[:, None], (K // 16, N))
+    z = np.tile((np.arange(N) % 16).astype(np.uint8), (K // G, 1))
+    s = np.tile(np.repeat(scales_1d, 16), (K // G, 1)).astype(np.float16)
+    out = oracle.int4_dequant(oracle.pack_int4(q), s, oracle.pack_int4(z), G)
+    for n in range(0, N, 7):
+        sv = float(scales_1d[n // 16])
+        for k in range(16):
+            d = int(q[k, n]) - int(z[0, n])
+            # IEEE: the exact zero q - z = +0 times s carries the sign of s
+            exact = float(d * Fraction(sv)) if d else math.copysign(0.0, sv)
+            assert out.view(np.uint16)[k, n] == f16_rne(exact), (k, n)
+
+
+def test_dequant_group_indexing_brute_force():
+    """Distinct scales and zero-points per group and column: element (k, n) must use
+    group k // G (a k % G or transposed lookup fails)."""
+    rng = np.random.default_rng(2)
+    K, N, G = 12, 6, 4
+    q = rng.integers(0, 16, (K, N), dtype=np.uint8)
+    z = rng.integers(0, 16, (K // G, N), dtype=np.uint8)
+    s = (rng.random((K // G, N)) * 0.01 + 0.001).astype(np.float16)
+    out = oracle.int4_dequant(oracle.pack_int4(q), s, oracle.pack_int4(z), G)
+    for k, n in itertools.product(range(K), range(N)):
+        exact = (int(q[k, n]) - int(z[k // G, n])) * Fraction(float(s[k // G, n]))
+        assert out.view(np.uint16)[k, n] == f16_rne(float(exact))
+
+
+# ----------------------------------------------------------------------------- bf16 / e4m3 casts
+
+
+def test_bf16_matches_torch():
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32),
+                        rng.integers(0, 2**32, 100000, dtype=np.uint64).astype(np.uint32).view(np.float32),
+                        np.array([0.0, -0.0, np.inf, -np.inf, 3.3895314e38, 1e-45], np.float32)])
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    got = oracle.f32_to_bf16_bits(x)
+    finite = np.isfinite(x)
+    assert np.array_equal(got[finite], ref[finite])
+    assert np.isnan(oracle.bf16_bits_to_f32(got[~np.isfinite(x) & np.isnan(x)])).all()
+
+
+@pytest.mark.parametrize("scale", [1.0, 1.0 / 3.0, 7.3, 1e-3, 300.0, 2.0 ** -12])
+def test_e4m3_every_fp16_value_matches_torch(scale):
+    h = np.arange(65536, dtype=np.uint16).view(np.float16).astype(np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        x = (h * np.float32(scale)).astype(np.float32)
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(oracle.e4m3_from_f32(x), ref)
+
+
+def test_e4m3_rounding_boundaries_match_torch():
+    """Every midpoint between adjacent e4m3 values (and the 448/464/480 overflow
+    edges), +-0..3 fp32 ulps, both signs."""
+    vals = oracle.e4m3_to_f32(np.arange(0x7F, dtype=np.uint8)).astype(np.float64)  # 0 .. 448
+    mids = list((vals[:-1] + vals[1:]) / 2) + [448.0, 464.0, 480.0, 2.0 ** -10, 2.0 ** -6]
+    base = np.array(mids, np.float32).view(np.uint32).astype(np.int64)
+    bits = (base[:, None] + np.arange(-3, 4)[None, :]).ravel()
+    bits = bits[(bits >= 0) & (bits < 0x7F800000)].astype(np.uint32)
+    x = np.concatenate([bits, bits | 0x80000000]).view(np.float32)
+    ref = torch.from_numpy(x.copy()).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(oracle.e4m3_from_f32(x), ref)
+
+
+def test_e4m3_random_bit_patterns_and_decode_match_torch():
+    r = np.random.default_rng(4).integers(0, 2**32, 2_000_000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    ref = torch.from_numpy(r.copy()).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(oracle.e4m3_from_f32(r), ref)
+    codes = np.arange(256, dtype=np.uint8)
+    dec = torch.from_numpy(codes).view(torch.float8_e4m3fn).to(torch.float32).numpy()
+    mine = oracle.e4m3_to_f32(codes)
+    assert np.array_equal(np.isnan(dec), np.isnan(mine))
+    assert np.array_equal(dec[~np.isnan(dec)], mine[~np.isnan(mine)])
+    ok = ~np.isnan(mine)
+    assert np.array_equal(oracle.e4m3_from_f32(mine[ok]), codes[ok])   # exact values round-trip
+
+
+# ----------------------------------------------------------------------------- fp8 quant
+
+
+def test_fp8_quant_matches_torch_cast_path():
+    rng = np.random.default_rng(5)
+    A = (rng.standard_normal((64, 512)) * np.exp(rng.standard_normal((64, 1)) * 3)).astype(np.float16)
+    codes, sa = oracle.fp8_act_quant(A)
+    t = torch.from_numpy(A)
+    amax = t.abs().amax(dim=1).float()
+    tsa = amax / 448.0
+    tq = (t.float() / tsa[:, None]).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(sa.view(np.uint32), tsa.numpy().view(np.uint32))
+    assert np.array_equal(codes, tq)
+
+
+def test_fp8_quant_invariants():
+    rng = np.random.default_rng(6)
+    A = rng.standard_normal((32, 1024)).astype(np.float16)
+    A[3] = 0
+    codes, sa = oracle.fp8_act_quant(A)
+    assert (codes[3] == 0xFF).all() and sa[3] == 0
+    rows = [r for r in range(32) if r != 3]
+    # the row maximum lands on +-448 (0x7E / 0xFE); no other code exceeds it
+    for r in rows:
+        j = int(np.argmax(np.abs(A[r].astype(np.float32))))
+        assert codes[r, j] & 0x7F == 0x7E
+        assert ((codes[r] & 0x7F) <= 0x7E).all()
+    # reconstruction error within half an e4m3 step of the scaled value
+    deq = oracle.e4m3_to_f32(codes[rows]).astype(np.float64) * sa[rows, None]
+    x = A[rows].astype(np.float64)
+    q = np.abs(x / sa[rows, None])
+    e = np.floor(np.log2(np.maximum(q, 2.0 ** -6)))
+    half_step = 2.0 ** (e - 3) / 2 * sa[rows, None]
+    assert (np.abs(deq - x) <= half_step * (1 + 1e-6) + 1e-30).all()
+
+
+@pytest.mark.slow
+def test_fp8_quotient_scheme_exhaustive_c():
+    """The GPU kernel's reciprocal-refinement quotient equals the IEEE quotient on
+    its whole domain (every fp16 row max x every |x| <= max); the same program
+    with the sign fix removed must report mismatches."""
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    src = os.path.join(ROOT, "tests", "native", "fp8_quotient_check.c")
+    out = os.path.join(ROOT, "tests", "native", "_fp8_quotient_check")
+    bad = out + "_planted"
+    flags = ["-O2", "-ffp-contract=off", "-fno-fast-math", "-fopenmp"]
+    subprocess.run([gcc, *flags, src, "-lm", "-o", out], check=True)
+    subprocess.run([gcc, *flags, "-DPLANT_DROPPED_COPYSIGN", src, "-lm", "-o", bad], check=True)
+    try:
+        good = subprocess.run([out], capture_output=True, text=True, timeout=600)
+        assert good.returncode == 0, good.stdout
+        assert "mismatches=0" in good.stdout
+        planted = subprocess.run([bad], capture_output=True, text=True, timeout=600)
+        assert planted.returncode != 0 and "mismatches=0" not in planted.stdout
+    finally:
+        for f in (out, bad):
+            if os.path.exists(f):
+                os.remove(f)
+
+
+# ----------------------------------------------------------------------------- GEMMs
+
+
+def test_fp8_scaled_gemm_brute_force():
+    rng = np.random.default_rng(7)
+    M, K, N = 3, 5, 4
+    Aq = rng.integers(0, 0x7F, (M, K), dtype=np.uint8) | (rng.integers(0, 2, (M, K), dtype=np.uint8) << 7)
+    Wq = rng.integers(0, 0x7F, (K, N), dtype=np.uint8)
+    Aq[Aq & 0x7F == 0x7F] = 0x38
+    sa = rng.random(M).astype(np.float32) + 0.5
+    sw = rng.random(N).astype(np.float32) * 0.01
+    Y = oracle.bf16_bits_to_f32(oracle.fp8_scaled_gemm(Aq, Wq, sa, sw))
+    a, w = oracle.e4m3_to_f32(Aq), oracle.e4m3_to_f32(Wq)
+    for m, n in itertools.product(range(M), range(N)):
+        exact = sum(Fraction(float(a[m, k])) * Fraction(float(w[k, n])) for k in range(K))
+        ref = float(exact * Fraction(float(sa[m])) * Fraction(float(sw[n])))
+        assert abs(Y[m, n] - ref) <= abs(ref) * 2 ** -8 + 1e-30
+    # a transposed weight operand gives a different answer (layout is pinned)
+    assert not np.array_equal(oracle.fp8_scaled_gemm(Aq[:, :4], Wq[:4, :4].T.copy(), sa, sw),
+                              oracle.fp8_scaled_gemm(Aq[:, :4], Wq[:4, :4], sa, sw))
+
+
+def test_fp8_scaled_gemm_identity():
+    """Aq = identity (code 0x38 is 1.0): Y = bf16(sa[m] * sw[n] * W[m, n])."""
+    n = 8
+    Aq = np.where(np.eye(n, dtype=bool), 0x38, 0).astype(np.uint8)
+    Wq = np.random.default_rng(8).integers(0, 0x7E, (n, n), dtype=np.uint8)
+    sa = np.linspace(0.5, 2, n).astype(np.float32)
+    sw = np.linspace(1, 3, n).astype(np.float32)
+    expect = oracle.f32_to_bf16_bits((oracle.e4m3_to_f32(Wq).astype(np.float64) * sa[:, None] * sw[None, :]).astype(np.float32))
+    assert np.array_equal(oracle.fp8_scaled_gemm(Aq, Wq, sa, sw), expect)
+
+
+def test_w4a16_gemm_brute_force_float64():
+    rng = np.random.default_rng(9)
+    M, K, N, G = 3, 8, 6, 4
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    q = rng.integers(0, 16, (K, N), dtype=np.uint8)
+    z = rng.integers(0, 16, (K // G, N), dtype=np.uint8)
+    s = (rng.random((K // G, N)) * 0.01 + 0.001).astype(np.float16)
+    Y = oracle.w4a16_gemm(A, oracle.pack_int4(q), s, oracle.pack_int4(z), G)
+    for m, n in itertools.product(range(M), range(N)):
+        acc = 0.0
+        for k in range(K):
+            wv = float(np.float16((int(q[k, n]) - int(z[k // G, n])) * float(s[k // G, n])))
+            acc += float(A[m, k]) * wv
+        assert abs(float(Y[m, n]) - acc) <= 2e-3 * abs(acc) + 1e-4
+
+
+def test_grouped_gemm_equals_per_segment_and_validates():
+    rng = np.random.default_rng(10)
+    E, K, N, G = 3, 8, 4, 4
+    offs = np.array([0, 4, 4, 9])                # an empty expert segment in the middle
+    A = rng.standard_normal((9, K)).astype(np.float16)
+    P = rng.integers(0, 256, (E, K, N // 2), dtype=np.uint8)
+    S = (rng.random((E, K // G, N)) * 0.01).astype(np.float16)
+    Z = rng.integers(0, 256, (E, K // G, N // 2), dtype=np.uint8)
+    Y = oracle.moe_w4a16_grouped_gemm(A, P, S, Z, offs, G)
+    for e in range(E):
+        lo, hi = offs[e], offs[e + 1]
+        if hi > lo:
+            assert np.array_equal(Y[lo:hi], oracle.w4a16_gemm(A[lo:hi], P[e], S[e], Z[e], G))
+    with pytest.raises(ValueError):
+        oracle.moe_w4a16_grouped_gemm(A, P, S, Z, np.array([0, 5, 4, 9]), G)
+
+
+# ----------------------------------------------------------------------------- gating
+
+
+def test_gating_reference_worked_example():
+    """tilebench/problems/moe_topk_gating_current.md:19-37; the example lists the
+    indices in ascending order, the reference impl_torch (sorted=True) and this
+    oracle return them by descending logit."""
+    logits = np.array([[1.0, 2.0, 3.0, 4.0], [4.0, 3.0, 2.0, 1.0]], np.float32)
+    w, i = oracle.moe_topk_gating(logits, 2)
+    assert i.tolist() == [[3, 2], [0, 1]]
+    np.testing.assert_allclose(w, [[0.7311, 0.2689], [0.7311, 0.2689]], atol=1e-4)
+
+
+def test_gating_brute_force_with_ties():
+    rng = np.random.default_rng(11)
+    x = rng.integers(-2, 3, (200, 12)).astype(np.float32)
+    x[0, :] = 0.0
+    x[1, 3] = -0.0
+    w, idx = oracle.moe_topk_gating(x, 5)
+    for r in range(200):
+        order = sorted(range(12), key=lambda j: (-float(x[r, j]), j))[:5]
+        assert idx[r].tolist() == order
+        v = np.array([float(x[r, j]) for j in order])
+        e = np.exp(v - v.max())
+        np.testing.assert_allclose(w[r], e / e.sum(), rtol=1e-6, atol=1e-7)
+        assert abs(float(w[r].sum()) - 1.0) < 1e-6
+
+
+def test_gating_matches_full_softmax_renormalised():
+    """Softmax over all experts, then top-k and renormalisation (BASELINE wording)
+    equals the softmax over the k selected logits."""
+    x = np.random.default_rng(12).standard_normal((500, 64)).astype(np.float32)
+    w, idx = oracle.moe_topk_gating(x, 8)
+    full = np.exp(x.astype(np.float64) - x.max(1, keepdims=True))
+    full /= full.sum(1, keepdims=True)
+    sel = np.take_along_axis(full, idx, 1)
+    np.testing.assert_allclose(w, sel / sel.sum(1, keepdims=True), rtol=2e-6, atol=1e-7)
+
+
+def test_gating_nan_ranks_first_and_half_dtypes():
+    x = np.array([[0.5, np.nan, 2.0, 1.0]], np.float32)
+    _, idx = oracle.moe_topk_gating(x, 2)
+    assert idx.tolist() == [[1, 2]]
+    xb = oracle.f32_to_bf16_bits(np.array([[1.0, 3.0, 2.0]], np.float32))
+    wb, ib = oracle.moe_topk_gating(xb, 2, dtype="bf16")
+    assert ib.tolist() == [[1, 2]] and wb.dtype == np.uint16
+    wh, ih = oracle.moe_topk_gating(np.array([[1.0, 3.0, 2.0]], np.float16), 2, dtype="fp16")
+    assert ih.tolist() == [[1, 2]] and wh.dtype == np.float16
+    assert math.isclose(float(wh[0, 0]), 0.7311, abs_tol=1e-3)
