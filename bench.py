@@ -140,6 +140,33 @@ def _w_w4a16(M):
     return make
 
 
+def _w_fp8_gemm():
+    from tilebench_amd.data import tensors as T
+    from tilebench_amd.benchmarks.operators.fp8_scaled_gemm import impl_hip
+
+    M = N = K = 8192
+    flops = 2 * M * N * K
+    nbytes = M * K + K * N + 4 * M + 4 * N + 2 * M * N
+
+    def inputs():
+        return T.generate_fp8_scaled_gemm_inputs(M, N, K, seed=2, device="cuda")
+
+    def cpu_sample():
+        import oracle
+        import torch
+        rows = 32
+        Aq, Wq, sa, sw = T.generate_fp8_scaled_gemm_inputs(rows, N, K, seed=2, device="cpu")
+        a, w = Aq.view(torch.uint8).numpy(), Wq.contiguous().view(torch.uint8).numpy()
+        sa, sw = sa.numpy(), sw.numpy()
+        return ((lambda: oracle.fp8_scaled_gemm(a, w, sa, sw)), 2 * rows * N * K,
+                f"{rows} of {M} rows (numpy e4m3 decode + float64 BLAS matmul)")
+
+    return dict(name="fp8_scaled_gemm", config={"workload": "fp8_scaled_gemm", "M": M, "N": N, "K": K},
+                metric="fp8 row/column-scaled GEMM throughput", unit="TFLOP/s", dtype="e4m3 x e4m3 -> bf16 (fp32 acc)",
+                bound="mfma", peak_key="fp8", bytes=nbytes, flops=flops, out_bytes=2 * M * N, inputs=inputs,
+                step=lambda x: impl_hip.run(*x), kernel="fp8_gemm_kernel", cpu_sample=cpu_sample)
+
+
 def _w_copy():
     import torch
 
@@ -168,6 +195,7 @@ WORKLOADS = {
     "moe_topk_gating_E64": _w_gating(64),
     "moe_topk_gating_E256": _w_gating(256),
     "fp8_act_quant": _w_fp8_quant,
+    "fp8_scaled_gemm": _w_fp8_gemm,
     "hbm_copy_probe": _w_copy,
 }
 DEFAULT_OP = "w4a16_gemm_M4096"

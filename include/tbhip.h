@@ -113,6 +113,21 @@ tb_status tb_w4a16_gemm(const uint16_t* A, const uint8_t* W, const uint16_t* sca
 tb_status tb_w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int64_t group, int64_t* bytes);
 
 /*
+ * Row/column-scaled fp8 GEMM (step 2):
+ *   Y bf16 [M, N] = bf16(sa[m] * sw[n] * sum_k e4m3(Aq[m,k]) * e4m3(Wq[k,n])),
+ *   fp32 accumulation on the e4m3 matrix cores, one RNE rounding.
+ *   Aq uint8 [M, K] row-major; WqT uint8 [N, K] row-major (the K-contiguous
+ *   "column-major" weight layout); sa fp32 [M]; sw fp32 [N].
+ * Requires K % 128 == 0, N % 8 == 0, each operand < 2 GiB, Aq / WqT / Y
+ * 16-byte aligned.
+ * Replaces: matmul_fp32_fp16_fp8/impl_triton.py:124 run(a, b) for fp8_e4m3fn
+ * (torch._scaled_mm with unit scales and bf16 output in impl_torch.py:21-26),
+ * with per-row / per-column scales.
+ */
+tb_status tb_fp8_scaled_gemm(const uint8_t* Aq, const uint8_t* WqT, const float* sa, const float* sw, uint16_t* Y,
+                             int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+/*
  * Fill `bytes` bytes of `buf` with a 32-bit pattern using a plain store
  * kernel.  Used to evict the L2 and the 256 MiB MALL between timed launches
  * (a kernel, not hipMemset, so it may be captured into a graph).

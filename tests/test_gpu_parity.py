@@ -226,3 +226,76 @@ def test_w4a16_decode_alternating_inputs(gpu, M):
                                    atol=1e-2, rtol=1e-2, err_msg=f"call {i}")
     for i in range(2, 6):
         assert torch.equal(outs[i], outs[i % 2]), f"call {i} differs from call {i % 2}"
+
+
+# ----------------------------------------------------------------------------- fp8 GEMM
+
+def _fp8_gemm_check(gpu, M, N, K, seed):
+    from tilebench_amd.benchmarks.operators.fp8_scaled_gemm import impl_hip
+
+    _say("fp8_scaled_gemm", M, N, K)
+    Aq, Wq, sa, sw = T.generate_fp8_scaled_gemm_inputs(M, N, K, seed=seed, device="cpu")
+    Y = impl_hip.run(Aq.to(gpu), Wq.to(gpu), sa.to(gpu), sw.to(gpu))
+    torch.cuda.synchronize()
+    ref = oracle.bf16_bits_to_f32(oracle.fp8_scaled_gemm(Aq.view(torch.uint8).numpy(),
+                                                         Wq.contiguous().view(torch.uint8).numpy(),
+                                                         sa.numpy(), sw.numpy()))
+    got = Y.float().cpu().numpy()
+    np.testing.assert_allclose(got, ref, atol=1e-2, rtol=1e-2)
+    return got, ref
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 128), (512, 768, 1024), (300, 200, 256), (64, 8, 128),
+                                   (1024, 1024, 2048)])
+def test_fp8_gemm_matches_oracle(gpu, M, N, K):
+    _fp8_gemm_check(gpu, M, N, K, seed=M + N + K)
+
+
+def test_fp8_gemm_full_size_rows(gpu):
+    """BASELINE config 2 (8192^3): rows sampled against the oracle, all finite."""
+    from tilebench_amd.benchmarks.operators.fp8_scaled_gemm import impl_hip
+
+    M = N = K = 8192
+    _say("fp8_scaled_gemm full", M, N, K)
+    Aq, Wq, sa, sw = T.generate_fp8_scaled_gemm_inputs(M, N, K, seed=2, device="cpu")
+    Y = impl_hip.run(Aq.to(gpu), Wq.to(gpu), sa.to(gpu), sw.to(gpu)).float().cpu().numpy()
+    assert np.isfinite(Y).all()
+    rows = np.random.default_rng(1).choice(M, 48, replace=False)
+    ref = oracle.bf16_bits_to_f32(oracle.fp8_scaled_gemm(Aq.view(torch.uint8).numpy()[rows],
+                                                         Wq.contiguous().view(torch.uint8).numpy(),
+                                                         sa.numpy()[rows], sw.numpy()))
+    np.testing.assert_allclose(Y[rows], ref, atol=1e-2, rtol=1e-2)
+
+
+def test_golden_fixtures_on_gpu(gpu):
+    """Every committed golden fixture reproduced by the GPU kernels."""
+    import os
+    from tilebench_amd.benchmarks.operators.int4_dequant import impl_hip as dq
+    from tilebench_amd.benchmarks.operators.moe_topk_gating import impl_hip as gt
+    from tilebench_amd.benchmarks.operators.fp8_act_quant import impl_hip as fq
+    from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip as wg
+    from tilebench_amd.benchmarks.operators.fp8_scaled_gemm import impl_hip as fg
+
+    _say("golden fixtures")
+    gd = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    ld = lambda n: dict(np.load(os.path.join(gd, n + ".npz")))
+    d = lambda a: torch.from_numpy(a).to(gpu)
+    f = ld("int4_dequant")
+    K, N = f["out"].shape
+    out = dq.run(d(f["packed"]), d(f["scales"]), d(f["zeros"]), K, N, int(f["group"]))
+    np.testing.assert_array_equal(_u16(out), f["out"].view(np.uint16))
+    f = ld("moe_topk_gating")
+    w, i = gt.run(d(f["logits"]), *f["logits"].shape, int(f["k"]))
+    np.testing.assert_array_equal(i.cpu().numpy(), f["indices"])
+    np.testing.assert_allclose(w.cpu().numpy(), f["weights"], atol=1e-5, rtol=1e-5)
+    f = ld("fp8_act_quant")
+    q, sa = fq.run(d(f["A"]))
+    np.testing.assert_array_equal(q.cpu().view(torch.uint8).numpy(), f["codes"])
+    f = ld("w4a16_gemm")
+    Y = wg.run(d(f["A"]), d(f["packed"]), d(f["scales"]), d(f["zeros"]), int(f["group"]))
+    np.testing.assert_allclose(Y.cpu().numpy().astype(np.float32), f["Y"].astype(np.float32), atol=1e-2, rtol=1e-2)
+    f = ld("fp8_scaled_gemm")
+    aq = d(f["Aq"]).view(torch.float8_e4m3fn)
+    wq = d(np.ascontiguousarray(f["Wq"].T)).view(torch.float8_e4m3fn).t()
+    Y = fg.run(aq, wq, d(f["sa"]), d(f["sw"]))
+    np.testing.assert_allclose(Y.float().cpu().numpy(), oracle.bf16_bits_to_f32(f["Y"]), atol=1e-2, rtol=1e-2)
