@@ -167,6 +167,32 @@ def _w_fp8_gemm():
                 step=lambda x: impl_hip.run(*x), kernel="fp8_gemm_kernel", cpu_sample=cpu_sample)
 
 
+def _w_grouped():
+    from tilebench_amd.data import tensors as T
+    from tilebench_amd.benchmarks.operators.moe_w4a16_grouped_gemm import impl_hip
+
+    tokens, topk, E, K, N, G = 16384, 8, 64, 4096, 1408, 128
+    flops = 2 * tokens * topk * K * N
+    nbytes = 2 * tokens * topk * K + E * (K * N // 2 + (K // G) * N * 2 + (K // G) * N // 2) + 2 * tokens * topk * N
+
+    def inputs():
+        return T.generate_moe_w4a16_grouped_gemm_inputs(tokens, topk, E, K, N, G, seed=4, device="cuda")
+
+    def cpu_sample():
+        import oracle
+        A, p, s, z, off, _ = T.generate_moe_w4a16_grouped_gemm_inputs(256, 8, E, K, N, G, seed=4, device="cpu")
+        A, p, s, z, off = A.numpy(), p.numpy(), s.numpy(), z.numpy(), off.numpy()
+        return ((lambda: oracle.moe_w4a16_grouped_gemm(A, p, s, z, off, G)), 2 * 256 * 8 * K * N,
+                "256 of 16384 tokens x top-8 over all 64 experts (numpy dequant + fp32 BLAS)")
+
+    return dict(name="moe_w4a16_grouped_gemm",
+                config={"workload": "moe_w4a16_grouped_gemm", "tokens": tokens, "topk": topk, "experts": E, "K": K,
+                        "N": N, "group": G, "zipf_s": 1.1, "pad": 128},
+                metric="MoE grouped W4A16 GEMM throughput", unit="TFLOP/s", dtype="fp16 x int4 -> fp16 (fp32 acc)",
+                bound="mfma", peak_key="fp16", bytes=nbytes, flops=flops, out_bytes=2 * (tokens * topk + E * 128) * N,
+                inputs=inputs, step=lambda x: impl_hip.run(*x), kernel="w4a16_grouped", cpu_sample=cpu_sample)
+
+
 def _w_copy():
     import torch
 
@@ -196,6 +222,7 @@ WORKLOADS = {
     "moe_topk_gating_E256": _w_gating(256),
     "fp8_act_quant": _w_fp8_quant,
     "fp8_scaled_gemm": _w_fp8_gemm,
+    "moe_w4a16_grouped_gemm": _w_grouped,
     "hbm_copy_probe": _w_copy,
 }
 DEFAULT_OP = "w4a16_gemm_M4096"

@@ -113,6 +113,23 @@ tb_status tb_w4a16_gemm(const uint16_t* A, const uint8_t* W, const uint16_t* sca
 tb_status tb_w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int64_t group, int64_t* bytes);
 
 /*
+ * Grouped MoE W4A16 GEMM: rows offsets[e] .. offsets[e+1]
+ * of the expert-sorted activations A use expert e's int4 weights.
+ *   A fp16 [R, K]; W uint8 [E, K, N/2]; scales fp16 [E, K/G, N];
+ *   zeros uint8 [E, K/G, N/2]; offsets int32 [E+1] in device memory,
+ *   non-decreasing from 0 to R -> Y fp16 [R, N] (rows outside every segment are
+ *   left untouched).  Each expert's product is exactly tb_w4a16_gemm's.
+ * Requires N % 8 == 0, K % 64 == 0, G % 64 == 0, K % G == 0, E <= 4096,
+ * A < 4 GiB, one expert's W < 2 GiB; A, scales, Y 16-byte aligned.
+ * Replaces: no reference operator (the reference has no grouped GEMM); the
+ * nearest is matmul_fp32_fp16_fp8/impl_triton.py:124 run(a, b) applied per
+ * expert.
+ */
+tb_status tb_moe_w4a16_grouped_gemm(const uint16_t* A, const uint8_t* W, const uint16_t* scales,
+                                    const uint8_t* zeros, const int32_t* offsets, uint16_t* Y, int64_t R,
+                                    int64_t experts, int64_t N, int64_t K, int64_t group, hipStream_t stream);
+
+/*
  * Row/column-scaled fp8 GEMM (step 2):
  *   Y bf16 [M, N] = bf16(sa[m] * sw[n] * sum_k e4m3(Aq[m,k]) * e4m3(Wq[k,n])),
  *   fp32 accumulation on the e4m3 matrix cores, one RNE rounding.

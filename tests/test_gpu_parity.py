@@ -299,3 +299,57 @@ def test_golden_fixtures_on_gpu(gpu):
     wq = d(np.ascontiguousarray(f["Wq"].T)).view(torch.float8_e4m3fn).t()
     Y = fg.run(aq, wq, d(f["sa"]), d(f["sw"]))
     np.testing.assert_allclose(Y.float().cpu().numpy(), oracle.bf16_bits_to_f32(f["Y"]), atol=1e-2, rtol=1e-2)
+
+
+# ----------------------------------------------------------------------------- grouped MoE W4A16
+
+@pytest.mark.parametrize("tokens,topk,E,K,N,pad", [(512, 2, 8, 256, 1408, 128), (300, 4, 16, 512, 264, 16),
+                                                    (64, 1, 4, 128, 64, 64), (1000, 8, 64, 256, 512, 128)])
+def test_grouped_gemm_matches_oracle(gpu, tokens, topk, E, K, N, pad):
+    from tilebench_amd.benchmarks.operators.moe_w4a16_grouped_gemm import impl_hip
+
+    _say("moe_w4a16_grouped_gemm", tokens, topk, E, K, N, pad)
+    A, p, s, z, off, G = T.generate_moe_w4a16_grouped_gemm_inputs(tokens, topk, E, K, N, 128, pad=pad,
+                                                                  seed=tokens + E, device="cpu")
+    Y = impl_hip.run(A.to(gpu), p.to(gpu), s.to(gpu), z.to(gpu), off.to(gpu), G)
+    torch.cuda.synchronize()
+    ref = oracle.moe_w4a16_grouped_gemm(A.numpy(), p.numpy(), s.numpy(), z.numpy(), off.numpy(), G)
+    np.testing.assert_allclose(Y.cpu().numpy().astype(np.float32), ref.astype(np.float32), atol=1e-2, rtol=1e-2)
+
+
+def test_grouped_gemm_segments_equal_dense_kernel(gpu):
+    """Each expert's rows of the grouped product equal the dense W4A16 kernel on
+    that expert (bit for bit: same tile code, same summation order)."""
+    from tilebench_amd.benchmarks.operators.moe_w4a16_grouped_gemm import impl_hip as gg
+    from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip as wg
+
+    _say("grouped vs dense")
+    A, p, s, z, off, G = T.generate_moe_w4a16_grouped_gemm_inputs(2048, 8, 16, 1024, 1408, 128, pad=128,
+                                                                  seed=9, device="cpu")
+    Ad, pd, sd, zd = A.to(gpu), p.to(gpu), s.to(gpu), z.to(gpu)
+    Y = gg.run(Ad, pd, sd, zd, off.to(gpu), G)
+    o = off.tolist()
+    for e in (0, 3, 15):
+        lo, hi = o[e], o[e + 1]
+        if hi - lo > 16:
+            Ye = wg.run(Ad[lo:hi], pd[e], sd[e], zd[e], G)
+            assert torch.equal(Y[lo:hi], Ye), f"expert {e}"
+
+
+def test_grouped_gemm_full_config_rows(gpu):
+    """BASELINE config 4 (64 experts, 16384 tokens x top-8, Zipf 1.1): rows of the
+    heaviest and lightest experts checked against the oracle."""
+    from tilebench_amd.benchmarks.operators.moe_w4a16_grouped_gemm import impl_hip
+
+    _say("grouped full config 4")
+    A, p, s, z, off, G = T.generate_moe_w4a16_grouped_gemm_inputs(16384, 8, 64, 4096, 1408, 128, seed=4,
+                                                                  device="cpu")
+    Y = impl_hip.run(A.to(gpu), p.to(gpu), s.to(gpu), z.to(gpu), off.to(gpu), G).cpu().numpy()
+    o = off.numpy()
+    sizes = np.diff(o)
+    for e in (int(np.argmax(sizes)), int(np.argmin(np.where(sizes > 0, sizes, 1 << 30)))):
+        lo = o[e]
+        rows = slice(lo, min(lo + 64, o[e + 1]))
+        ref = oracle.w4a16_gemm(A.numpy()[rows], p.numpy()[e], s.numpy()[e], z.numpy()[e], G)
+        np.testing.assert_allclose(Y[rows].astype(np.float32), ref.astype(np.float32), atol=1e-2, rtol=1e-2)
+    assert np.isfinite(Y.astype(np.float32)).all()

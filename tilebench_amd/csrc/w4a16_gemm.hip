@@ -101,14 +101,17 @@ struct WRegs4 {
   uint32_t z;
 };
 
-__global__ void __launch_bounds__(T4, 1)
-    w4a16_prefill(const _Float16* __restrict__ A, const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
-                  const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int M, int N, int K, int group,
-                  int tiles_m, int tiles_n) {
-  extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+// One 256 x 256 tile: rows [m0, m_end) of A (A holds a_rows rows in all),
+// columns [n0, n0 + 256) of W (N columns), full K.  Shared by the dense kernel
+// and the grouped (MoE) kernel, which passes one expert's W / scales / zeros.
+__device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _Float16* __restrict__ A,
+                                             const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
+                                             const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int a_rows,
+                                             int m0, int m_end, int n0, int N, int K, int group) {
   _Float16* const lds_a = lds;
   _Float16* const lds_b = lds + A_STAGES * A_STAGE;
-  const Tile tile = tile_of_block(tiles_m, tiles_n);
+  const Tile tile{m0, n0};
+  const int M = m_end;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave >> 2, wn = wave & 3;
 
@@ -120,7 +123,7 @@ __global__ void __launch_bounds__(T4, 1)
     const uint64_t base = (uint64_t)(uintptr_t)A;
     ra4[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)base);
     ra4[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(base >> 32) & 0xFFFF);
-    ra4[2] = __builtin_amdgcn_readfirstlane((int)((uint32_t)M * (uint32_t)K * 2u));
+    ra4[2] = __builtin_amdgcn_readfirstlane((int)((uint32_t)a_rows * (uint32_t)K * 2u));
     ra4[3] = (int)RSRC_DW3;
   }
 
@@ -298,6 +301,49 @@ __global__ void __launch_bounds__(T4, 1)
       *reinterpret_cast<u32x4*>(Y + (int64_t)(tile.m0 + row) * N + tile.n0 + ch * 8) = v;
     }
   }
+}
+
+__global__ void __launch_bounds__(T4, 1)
+    w4a16_prefill(const _Float16* __restrict__ A, const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
+                  const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int M, int N, int K, int group,
+                  int tiles_m, int tiles_n) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+  const Tile tile = tile_of_block(tiles_m, tiles_n);
+  prefill_tile(lds, A, W, S, Z, Y, M, tile.m0, M, tile.n0, N, K, group);
+}
+
+// Grouped (MoE) variant: rows offsets[e] .. offsets[e+1] of A use expert e's
+// weights.  The grid is an upper bound (sum over experts of ceil(rows / 256)
+// <= R / 256 + E tile rows, times the N tiles); each block walks the E + 1
+// offsets to find its expert and tile row, and blocks past the last tile exit.
+// Tile ids are regrouped per XCD as in the dense kernel, so the blocks
+// resident on one XCD work on neighbouring tiles of the same expert.
+__global__ void __launch_bounds__(T4, 1)
+    w4a16_grouped(const _Float16* __restrict__ A, const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
+                  const uint8_t* __restrict__ Z, const int* __restrict__ offsets, _Float16* __restrict__ Y, int R,
+                  int experts, int N, int K, int group, int tiles_n) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+  const int nb = gridDim.x;
+  int bid = blockIdx.x;
+  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  const int mt = bid / tiles_n, nt = bid - mt * tiles_n;
+  int e = -1, m0 = 0, m_end = 0;
+  int seen = 0;
+  for (int x = 0; x < experts; ++x) {
+    // clamped to [0, R] so that malformed offsets can never address rows outside A / Y
+    const int lo = min(max(offsets[x], 0), R), hi = min(max(offsets[x + 1], lo), R);
+    const int cnt = (hi - lo + BM - 1) / BM;
+    if (mt < seen + cnt) {
+      e = x;
+      m0 = lo + (mt - seen) * BM;
+      m_end = hi;
+      break;
+    }
+    seen += cnt;
+  }
+  if (e < 0) return;  // beyond the last tile: uniform across the block
+  const int64_t wstride = (int64_t)K * (N / 2), sstride = (int64_t)(K / group) * N, zstride = (int64_t)(K / group) * (N / 2);
+  prefill_tile(lds, A, W + e * wstride, S + e * sstride, Z + e * zstride, Y, R, m0, m_end, nt * BN, N, K, group);
 }
 
 // ---------------------------------------------------------------------------
@@ -530,4 +576,41 @@ extern "C" tb_status tb_w4a16_gemm(const uint16_t* A, const uint8_t* W, const ui
                      reinterpret_cast<const _Float16*>(A), W, reinterpret_cast<const _Float16*>(scales), zeros,
                      reinterpret_cast<_Float16*>(Y), (int)M, (int)N, (int)K, (int)group, tiles_m, tiles_n);
   return tb::launch_status("tb_w4a16_gemm");
+}
+
+extern "C" tb_status tb_moe_w4a16_grouped_gemm(const uint16_t* A, const uint8_t* W, const uint16_t* scales,
+                                               const uint8_t* zeros, const int32_t* offsets, uint16_t* Y, int64_t R,
+                                               int64_t experts, int64_t N, int64_t K, int64_t group,
+                                               hipStream_t stream) {
+  using namespace tb::w4a16;
+  TB_CHECK_ARG(A && W && scales && zeros && offsets && Y, "tb_moe_w4a16_grouped_gemm: null pointer");
+  TB_CHECK_ARG(R > 0 && experts > 0 && N > 0 && K > 0 && group > 0, "tb_moe_w4a16_grouped_gemm: sizes must be positive");
+  TB_CHECK_ARG(experts <= 4096, "tb_moe_w4a16_grouped_gemm: at most 4096 experts (got %lld)", (long long)experts);
+  TB_CHECK_ARG(N % 8 == 0, "tb_moe_w4a16_grouped_gemm: N must be a multiple of 8 (got %lld)", (long long)N);
+  TB_CHECK_ARG(K % BK == 0 && group % BK == 0 && K % group == 0,
+               "tb_moe_w4a16_grouped_gemm: need K %% 64 == 0, group %% 64 == 0 and K %% group == 0");
+  TB_CHECK_ARG(R * K * 2 < (1ll << 31) * 2 - 1, "tb_moe_w4a16_grouped_gemm: A must be smaller than 4 GiB");
+  TB_CHECK_ARG(K * (N / 2) < (1ll << 31), "tb_moe_w4a16_grouped_gemm: one expert's weights must be < 2 GiB");
+  TB_CHECK_ALIGN(A, 16, "A");
+  TB_CHECK_ALIGN(W, 4, "W");
+  TB_CHECK_ALIGN(scales, 16, "scales");
+  TB_CHECK_ALIGN(zeros, 4, "zeros");
+  TB_CHECK_ALIGN(Y, 16, "Y");
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a16_grouped), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)LDS4_BYTES) != hipSuccess) {
+      tb::set_error("tb_moe_w4a16_grouped_gemm: cannot reserve %zu bytes of LDS", LDS4_BYTES);
+      return TB_E_HIP;
+    }
+    attr_set = true;
+  }
+  const int64_t tiles_n = (N + BN - 1) / BN;
+  const int64_t tile_rows = (R + BM - 1) / BM + experts;  // upper bound on sum_e ceil(rows_e / 256)
+  const int64_t blocks = tile_rows * tiles_n;
+  TB_CHECK_ARG(blocks < (1ll << 31), "tb_moe_w4a16_grouped_gemm: problem too large");
+  hipLaunchKernelGGL(w4a16_grouped, dim3((unsigned)blocks), dim3(T4), LDS4_BYTES, stream,
+                     reinterpret_cast<const _Float16*>(A), W, reinterpret_cast<const _Float16*>(scales), zeros, offsets,
+                     reinterpret_cast<_Float16*>(Y), (int)R, (int)experts, (int)N, (int)K, (int)group, (int)tiles_n);
+  return tb::launch_status("tb_moe_w4a16_grouped_gemm");
 }
