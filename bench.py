@@ -60,7 +60,7 @@ def _w_int4_dequant():
     return dict(name="int4_dequant", config={"workload": "int4_dequant", "K": K, "N": N, "group": G},
                 metric="int4 dequant HBM throughput", unit="GB/s", dtype="int4->fp16", bound="hbm",
                 bytes=nbytes, flops=2 * K * N, inputs=inputs, step=lambda x: impl_hip.run(*x),
-                kernel="int4_dequant_vec", cpu_sample=cpu_sample)
+                kernel="tb::int4_dequant_vec<8>", cpu_sample=cpu_sample)
 
 
 def _w_gating(E):
@@ -81,7 +81,7 @@ def _w_gating(E):
 
         return dict(name=f"moe_topk_gating_E{E}", config={"workload": "moe_topk_gating", "M": M, "E": E, "k": k},
                     metric="MoE gating HBM throughput", unit="GB/s", dtype="fp32", bound="hbm", bytes=nbytes,
-                    flops=None, inputs=inputs, step=lambda x: impl_hip.run(*x), kernel="gating_kernel",
+                    flops=None, inputs=inputs, step=lambda x: impl_hip.run(*x), kernel="tb::gating_kernel<0, 16, 4, 8>" if E <= 64 else "tb::gating_kernel<0, 64, 4, 8>",
                     cpu_sample=cpu_sample)
     return make
 
@@ -104,7 +104,7 @@ def _w_fp8_quant():
 
     return dict(name="fp8_act_quant", config={"workload": "fp8_act_quant", "M": M, "K": K},
                 metric="fp8 per-token quant HBM throughput", unit="GB/s", dtype="fp16->e4m3", bound="hbm",
-                bytes=nbytes, flops=None, inputs=inputs, step=lambda x: impl_hip.run(*x), kernel="fp8_quant_rows",
+                bytes=nbytes, flops=None, inputs=inputs, step=lambda x: impl_hip.run(*x), kernel="tb::fp8_quant_rows<4>",
                 cpu_sample=cpu_sample)
 
 
@@ -136,7 +136,7 @@ def _w_w4a16(M):
                     unit="TFLOP/s" if big else "GB/s", dtype="fp16 x int4 -> fp16 (fp32 acc)",
                     bound="mfma" if big else "hbm", peak_key="fp16", bytes=nbytes, flops=flops, out_bytes=2 * M * N,
                     inputs=inputs, step=lambda x: impl_hip.run(*x),
-                    kernel="w4a16_prefill" if big else "w4a16_decode", cpu_sample=cpu_sample)
+                    kernel="tb::w4a16::w4a16_prefill" if big else "tb::w4a16::w4a16_decode", cpu_sample=cpu_sample)
     return make
 
 
@@ -164,7 +164,7 @@ def _w_fp8_gemm():
     return dict(name="fp8_scaled_gemm", config={"workload": "fp8_scaled_gemm", "M": M, "N": N, "K": K},
                 metric="fp8 row/column-scaled GEMM throughput", unit="TFLOP/s", dtype="e4m3 x e4m3 -> bf16 (fp32 acc)",
                 bound="mfma", peak_key="fp8", bytes=nbytes, flops=flops, out_bytes=2 * M * N, inputs=inputs,
-                step=lambda x: impl_hip.run(*x), kernel="fp8_gemm_kernel", cpu_sample=cpu_sample)
+                step=lambda x: impl_hip.run(*x), kernel="tb::fp8gemm::fp8_gemm_kernel", cpu_sample=cpu_sample)
 
 
 def _w_grouped():
@@ -190,7 +190,7 @@ def _w_grouped():
                         "N": N, "group": G, "zipf_s": 1.1, "pad": 128},
                 metric="MoE grouped W4A16 GEMM throughput", unit="TFLOP/s", dtype="fp16 x int4 -> fp16 (fp32 acc)",
                 bound="mfma", peak_key="fp16", bytes=nbytes, flops=flops, out_bytes=2 * (tokens * topk + E * 128) * N,
-                inputs=inputs, step=lambda x: impl_hip.run(*x), kernel="w4a16_grouped", cpu_sample=cpu_sample)
+                inputs=inputs, step=lambda x: impl_hip.run(*x), kernel="tb::w4a16::w4a16_grouped", cpu_sample=cpu_sample)
 
 
 def _w_copy():
@@ -210,7 +210,7 @@ def _w_copy():
 
     return dict(name="hbm_copy_probe", config={"workload": "hbm_copy_probe", "bytes": nbytes},
                 metric="HBM streaming copy (calibration probe)", unit="GB/s", dtype="u8", bound="hbm", bytes=nbytes,
-                flops=None, out_bytes=nbytes // 2, inputs=inputs, step=step, kernel="copy_kernel", cpu_sample=None)
+                flops=None, out_bytes=nbytes // 2, inputs=inputs, step=step, kernel="tb::copy_kernel", cpu_sample=None)
 
 
 WORKLOADS = {
@@ -280,6 +280,18 @@ def time_steps(w, sets, steps: int, warmup: int):
     return ms
 
 
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (profiles/traffic.json), or None if it was not profiled."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            k = json.load(f)["kernels"].get(kernel)
+    except (OSError, ValueError, KeyError):
+        return None
+    return None if k is None else int(k["fetch_bytes"] + k["write_bytes"])
+
+
 def roofline(w, ms: float) -> dict:
     if w["bound"] == "hbm":
         achieved = w["bytes"] / (ms * 1e-3) / 1e9
@@ -288,7 +300,8 @@ def roofline(w, ms: float) -> dict:
         achieved = w["flops"] / (ms * 1e-3) / 1e12
         peak, unit = PEAK_TFLOPS[w["peak_key"]], "TFLOP/s"
     return {"bound": w["bound"], "achieved": round(achieved, 2), "peak": peak, "unit": unit,
-            "frac": round(achieved / peak, 4), "traffic": w.get("traffic")}
+            "frac": round(achieved / peak, 4), "traffic": measured_traffic(w["kernel"]),
+            "kernel": w["kernel"]}
 
 
 def cpu_baseline(w, budget_s: float = 10.0) -> dict:
@@ -333,6 +346,7 @@ def main(argv=None) -> int:
     ap.add_argument("--op", default=DEFAULT_OP, choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--suite", action="store_true", help="also measure every other workload")
+    ap.add_argument("--only", default=None, help="comma-separated workloads for --suite (default: all)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path.",
@@ -360,7 +374,8 @@ def main(argv=None) -> int:
     }
     if args.suite:
         suite = {}
-        for name in WORKLOADS:
+        names = args.only.split(",") if args.only else list(WORKLOADS)
+        for name in names:
             if name == args.op:
                 continue
             r = measure(name, args.steps, args.warmup, False)
