@@ -140,7 +140,6 @@ __global__ void __launch_bounds__(THREADS, 1)
     return r;
   };
 
-  constexpr int WAIT_VM8 = 8 | (7 << 4) | (15 << 8);
   constexpr int WAIT_VM0 = 0 | (7 << 4) | (15 << 8);
   const int nk = K / BK;
   issue(0);
@@ -151,18 +150,36 @@ __global__ void __launch_bounds__(THREADS, 1)
     if (more) issue(kt + 1);
     const uint8_t* sa_ = lds + (kt & 1) * 2 * STAGE;
     const uint8_t* sb_ = sa_ + STAGE;
+    {
+      // Both k64 substeps' fragments are read up front; the scheduling hints
+      // then interleave the second substep's 12 LDS reads with the first
+      // substep's MFMAs, so the matrix pipe does not wait on LDS latency.
+      i32x8 fa0[4], fb0[2], fa1[4], fb1[2];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      i32x8 fa[4], fb[2];
+      for (int i = 0; i < 4; ++i) fa0[i] = frag(sa_, a_row + i * 32, 0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) fa[i] = frag(sa_, a_row + i * 32, s);
+      for (int j = 0; j < 2; ++j) fb0[j] = frag(sb_, b_row + j * 32, 0);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) fb[j] = frag(sb_, b_row + j * 32, s);
+      for (int i = 0; i < 4; ++i) fa1[i] = frag(sa_, a_row + i * 32, 1);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) fb1[j] = frag(sb_, b_row + j * 32, 1);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[i], fb[j], acc[i][j], 0, 0, 0, 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa0[i], fb0[j], acc[i][j], 0, 0, 0, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa1[i], fb1[j], acc[i][j], 0, 0, 0, 0, 0, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);  // substep-0 fragment reads
+#pragma unroll
+      for (int q = 0; q < 6; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two substep-1 reads
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 10, 0);
     }
     // Stage kt+1 (issued above, 8 DMA per lane) must land before the barrier
     // that hands it to the next step.
