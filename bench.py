@@ -193,6 +193,73 @@ def _w_grouped():
                 inputs=inputs, step=lambda x: impl_hip.run(*x), kernel="tb::w4a16::w4a16_grouped", cpu_sample=cpu_sample)
 
 
+def _w_weight_dequant():
+    import torch
+    from tilebench_amd.data import tensors as T
+    from tilebench_amd.benchmarks.operators.weight_dequant import impl_hip
+
+    M, TS = 10240, 128
+    nbytes = 2 * M * M * 2 + ((M + TS - 1) // TS) ** 2 * 2   # weight_dequant/config.yaml bytes_expr, fp16
+
+    def inputs():
+        return T.generate_weight_dequant_inputs(M, TS, dtype=torch.float16, seed=10, device="cuda")
+
+    def cpu_sample():
+        import oracle
+        rows = 1024
+        X, S, *_ = T.generate_weight_dequant_inputs(rows, TS, dtype=torch.float16, N=M, seed=10, device="cpu")
+        X, S = X.numpy(), S.numpy()
+        return (lambda: oracle.weight_dequant(X, S, TS, "fp16")), 4 * rows * M, f"{rows} of {M} rows, fp16, numpy"
+
+    return dict(name="weight_dequant", config={"workload": "weight_dequant", "M": M, "TILE_SIZE": TS, "dtype": "fp16"},
+                metric="weight_dequant HBM throughput", unit="GB/s", dtype="fp16", bound="hbm", bytes=nbytes,
+                flops=M * M, inputs=inputs, step=lambda x: impl_hip.run(*x), kernel="tb::analog::weight_dequant_vec<1>",
+                cpu_sample=cpu_sample)
+
+
+def _w_dequantize_rowwise():
+    from tilebench_amd.data import tensors as T
+    from tilebench_amd.benchmarks.operators.dequantize_rowwise import impl_hip
+
+    rows, cols = 4096, 8192
+    nbytes = rows * cols + rows * 4 + rows * cols * 2            # dequantize_rowwise/config.yaml bytes_expr
+
+    def inputs():
+        return T.generate_dequantize_rowwise_inputs(rows, cols, seed=11, device="cuda")
+
+    def cpu_sample():
+        import oracle
+        x, st = T.generate_dequantize_rowwise_inputs(rows, cols, seed=11, device="cpu")
+        x, st = x.numpy(), st.numpy()
+        return (lambda: oracle.dequantize_rowwise(x, st)), nbytes, "full 4096x8192, numpy"
+
+    return dict(name="dequantize_rowwise", config={"workload": "dequantize_rowwise", "rows": rows, "cols": cols},
+                metric="dequantize_rowwise HBM throughput", unit="GB/s", dtype="int8->fp16", bound="hbm",
+                bytes=nbytes, flops=2 * rows * cols, inputs=inputs, step=lambda x: impl_hip.run(*x),
+                kernel="tb::analog::dequant_rowwise_vec", cpu_sample=cpu_sample)
+
+
+def _w_quantize_global():
+    from tilebench_amd.data import tensors as T
+    from tilebench_amd.benchmarks.operators.quantize_global import impl_hip
+
+    n = 20 * 1024 * 1024
+    nbytes = n * 4 + n * 2
+
+    def inputs():
+        return T.generate_quantize_global_inputs(n, seed=12, device="cuda")
+
+    def cpu_sample():
+        import oracle
+        x = T.generate_quantize_global_inputs(n, seed=12, device="cpu")[0].numpy()
+        return (lambda: oracle.quantize_global(x)), nbytes, "full n=20Mi, numpy"
+
+    return dict(name="quantize_global", config={"workload": "quantize_global", "n": n},
+                metric="quantize_global HBM throughput", unit="GB/s", dtype="fp32->fp16", bound="hbm", bytes=nbytes,
+                flops=None, inputs=inputs, step=lambda x: impl_hip.run(*x), kernel="tb::analog::f32_to_f16_vec",
+                cpu_sample=cpu_sample)
+
+
 def _w_copy():
     import torch
 
@@ -223,6 +290,9 @@ WORKLOADS = {
     "fp8_act_quant": _w_fp8_quant,
     "fp8_scaled_gemm": _w_fp8_gemm,
     "moe_w4a16_grouped_gemm": _w_grouped,
+    "weight_dequant": _w_weight_dequant,
+    "dequantize_rowwise": _w_dequantize_rowwise,
+    "quantize_global": _w_quantize_global,
     "hbm_copy_probe": _w_copy,
 }
 DEFAULT_OP = "w4a16_gemm_M4096"

@@ -145,6 +145,26 @@ tb_status tb_fp8_scaled_gemm(const uint8_t* Aq, const uint8_t* WqT, const float*
                              int64_t M, int64_t N, int64_t K, hipStream_t stream);
 
 /*
+ * The reference's own elementwise dequantisation / quantisation operators.
+ * Each product is formed in fp32 and rounded once to the output type (RNE), in
+ * the PyTorch reference's order of operations (bit-identical results).
+ *
+ * tb_weight_dequant: Y[i,j] = X[i,j] * S[i/T, j/T]; X, Y [M, N], S [ceil(M/T),
+ *   ceil(N/T)], all of `dtype` (0 fp32, 1 fp16, 2 bf16).
+ *   Replaces: weight_dequant/impl_triton.py:43 run(X, S, M, N, TILE_SIZE).
+ * tb_dequantize_rowwise: y fp16 [rows, cols] = fp16((state[r] * x[r,c]) * (1/127)),
+ *   x int8, state fp32 [rows].
+ *   Replaces: dequantize_rowwise/impl_triton.py:43 run(x, state_x).
+ * tb_quantize_global: y fp16 [n] = fp16(x fp32 [n]).
+ *   Replaces: quantize_global/impl_triton.py:31 run(x).
+ */
+tb_status tb_weight_dequant(const void* X, const void* S, void* Y, int64_t M, int64_t N, int64_t tile, int dtype,
+                            hipStream_t stream);
+tb_status tb_dequantize_rowwise(const int8_t* x, const float* state, uint16_t* y, int64_t rows, int64_t cols,
+                                hipStream_t stream);
+tb_status tb_quantize_global(const float* x, uint16_t* y, int64_t n, hipStream_t stream);
+
+/*
  * Fill `bytes` bytes of `buf` with a 32-bit pattern using a plain store
  * kernel.  Used to evict the L2 and the 256 MiB MALL between timed launches
  * (a kernel, not hipMemset, so it may be captured into a graph).

@@ -21,6 +21,9 @@ BASELINE config text):
                       with per-row / per-column scales instead of unit scales.
 * MoE gating        — moe_topk_gating/impl_torch.py:4-20 (topk, softmax over the k
                       values in fp32, int32 indices) with ties -> lowest index.
+* weight_dequant    — weight_dequant/impl_torch.py:4-8; dequantize_rowwise —
+                      dequantize_rowwise/impl_torch.py:4-7; quantize_global —
+                      quantize_global/impl_torch.py:4-5 (the reference's own operators).
 
 How each function is pinned (tests/test_oracle.py): closed forms and exact
 rational arithmetic (dequant), the torch CPU fp8 cast over every fp16 value and
@@ -41,4 +44,7 @@ from .core import (  # noqa: F401
     pack_int4,
     unpack_int4,
     w4a16_gemm,
+    weight_dequant,
+    dequantize_rowwise,
+    quantize_global,
 )

@@ -210,3 +210,36 @@ def moe_topk_gating(logits: np.ndarray, k: int, dtype: str = "fp32"):
     elif dtype == "bf16":
         w = f32_to_bf16_bits(w)
     return w, order.astype(np.int32)
+
+
+# ----------------------------------------------------------------------------- reference analog operators
+
+
+def weight_dequant(X: np.ndarray, S: np.ndarray, tile: int, dtype: str = "fp16") -> np.ndarray:
+    """Y[i, j] = X[i, j] * S[i // T, j // T] in the tensors' dtype ("fp32", "fp16",
+    or "bf16" with uint16 bit patterns): the product of two such values is exact
+    in fp32, then rounded once to the dtype."""
+    if dtype == "bf16":
+        x, s = bf16_bits_to_f32(X), bf16_bits_to_f32(S)
+    else:
+        x, s = np.asarray(X).astype(np.float32), np.asarray(S).astype(np.float32)
+    M, N = x.shape
+    full = np.repeat(np.repeat(s, tile, axis=0)[:M], tile, axis=1)[:, :N]
+    y = (x * full).astype(np.float32)
+    if dtype == "fp16":
+        return y.astype(np.float16)
+    if dtype == "bf16":
+        return f32_to_bf16_bits(y)
+    return y
+
+
+def dequantize_rowwise(x: np.ndarray, state: np.ndarray) -> np.ndarray:
+    """fp16((state[r] * x[r, c]) * (1/127)), two fp32 roundings then one to fp16."""
+    prod = (np.asarray(state, np.float32)[:, None] * np.asarray(x).astype(np.float32)).astype(np.float32)
+    return (prod * np.float32(1.0 / 127.0)).astype(np.float32).astype(np.float16)
+
+
+def quantize_global(x: np.ndarray) -> np.ndarray:
+    """fp32 -> fp16, round to nearest even (overflow -> inf)."""
+    with np.errstate(over="ignore"):
+        return np.asarray(x, np.float32).astype(np.float16)

@@ -353,3 +353,50 @@ def test_grouped_gemm_full_config_rows(gpu):
         ref = oracle.w4a16_gemm(A.numpy()[rows], p.numpy()[e], s.numpy()[e], z.numpy()[e], G)
         np.testing.assert_allclose(Y[rows].astype(np.float32), ref.astype(np.float32), atol=1e-2, rtol=1e-2)
     assert np.isfinite(Y.astype(np.float32)).all()
+
+
+# ----------------------------------------------------------------------------- reference analog operators
+
+@pytest.mark.parametrize("M,N,tile_size,dt", [(512, 512, 128, "fp16"), (1000, 1000, 128, "bf16"),
+                                               (2048, 2048, 128, "fp32"), (37, 45, 7, "fp16"), (64, 96, 16, "bf16"),
+                                               (10240, 10240, 128, "fp16")])
+def test_weight_dequant_matches_oracle(gpu, M, N, tile_size, dt):
+    from tilebench_amd.benchmarks.operators.weight_dequant import impl_hip
+
+    _say("weight_dequant", M, N, tile_size, dt)
+    tdt = {"fp32": torch.float32, "fp16": torch.float16, "bf16": torch.bfloat16}[dt]
+    X, S, M, N, tile = T.generate_weight_dequant_inputs(M, tile_size, dtype=tdt, N=N, seed=M, device="cpu")
+    Y = impl_hip.run(X.to(gpu), S.to(gpu), M, N, tile)
+    torch.cuda.synchronize()
+    if dt == "bf16":
+        ref = oracle.weight_dequant(X.view(torch.int16).numpy().view(np.uint16),
+                                    S.view(torch.int16).numpy().view(np.uint16), tile, dt)
+        np.testing.assert_array_equal(_u16(Y), ref)
+    else:
+        ref = oracle.weight_dequant(X.numpy(), S.numpy(), tile, dt)
+        got = Y.cpu().numpy()
+        np.testing.assert_array_equal(got.view(np.uint32 if dt == "fp32" else np.uint16),
+                                      ref.view(np.uint32 if dt == "fp32" else np.uint16))
+
+
+@pytest.mark.parametrize("rows,cols", [(512, 512), (4096, 8192), (33, 100), (7, 16)])
+def test_dequantize_rowwise_matches_oracle(gpu, rows, cols):
+    from tilebench_amd.benchmarks.operators.dequantize_rowwise import impl_hip
+
+    _say("dequantize_rowwise", rows, cols)
+    x, s = T.generate_dequantize_rowwise_inputs(rows, cols, seed=rows + cols, device="cpu")
+    y = impl_hip.run(x.to(gpu), s.to(gpu))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_u16(y), oracle.dequantize_rowwise(x.numpy(), s.numpy()).view(np.uint16))
+
+
+@pytest.mark.parametrize("n", [1 << 20, 20 * (1 << 20), 1001, 3])
+def test_quantize_global_matches_oracle(gpu, n):
+    from tilebench_amd.benchmarks.operators.quantize_global import impl_hip
+
+    _say("quantize_global", n)
+    (x,) = T.generate_quantize_global_inputs(n, seed=n % 97, device="cpu")
+    x[: min(n, 8)] = torch.tensor([65504.0, 65520.0, -1e-8, 2.0 ** -24, 2.0 ** -25, 3.0 * 2.0 ** -26, 1e30, -0.0])[: min(n, 8)]
+    y = impl_hip.run(x.to(gpu))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_u16(y), oracle.quantize_global(x.numpy()).view(np.uint16))

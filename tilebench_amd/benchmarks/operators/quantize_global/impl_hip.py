@@ -1,0 +1,22 @@
+"""hip backend of quantize_global: tb_quantize_global in libtbhip.so.  block_size
+is accepted for the reference signature (the engine passes it) and ignored: the
+kernel always moves 16-byte vectors."""
+import torch
+
+from tilebench_amd import runtime as rt
+
+rt.load_library()
+
+
+def run(x: torch.Tensor, block_size: int = 1024, **kwargs):
+    rt.require_device()
+    if x.dtype != torch.float32:
+        raise TypeError("quantize_global expects fp32 input")
+    x = x.contiguous()
+    y = torch.empty(x.shape, dtype=torch.float16, device=x.device)
+    rt.call("tb_quantize_global", x.data_ptr(), y.data_ptr(), x.numel(), rt.stream_handle(x.device))
+    return y
+
+
+def get_last_config():
+    return {"kernel": "f32_to_f16_vec", "elements_per_thread": 8}

@@ -39,6 +39,9 @@ SIGNATURES: dict[str, list] = {
     "tb_w4a16_workspace_size": [_c_i64, _c_i64, _c_i64, _c_i64, ctypes.POINTER(_c_i64)],
     "tb_moe_w4a16_grouped_gemm": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p],
     "tb_fp8_scaled_gemm": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p],
+    "tb_weight_dequant": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p],
+    "tb_dequantize_rowwise": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_p],
+    "tb_quantize_global": [_c_p, _c_p, _c_i64, _c_p],
     "tb_l2_flush": [_c_p, _c_i64, _c_u32, _c_p],
     "tb_probe_copy": [_c_p, _c_p, _c_i64, _c_p],
     "tb_probe_mfma": [_c_int, _c_i64, _c_i64, _c_p, _c_p],
