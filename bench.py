@@ -86,6 +86,30 @@ def _w_gating(E):
     return make
 
 
+def _w_gating_reference_grid():
+    import torch
+    from tilebench_amd.data import tensors as T
+    from tilebench_amd.benchmarks.operators.moe_topk_gating import impl_hip
+
+    M, E, k = 20480, 128, 2
+    nbytes = M * E * 2 + M * k * 2 + M * k * 4       # moe_topk_gating/config.yaml bytes_expr, fp16
+
+    def inputs():
+        return T.generate_moe_topk_gating_inputs(M, E, k, dtype=torch.float16, dist="grid", seed=3, device="cuda")
+
+    def cpu_sample():
+        import oracle
+        lg = T.generate_moe_topk_gating_inputs(M, E, k, dtype=torch.float16, dist="grid", seed=3,
+                                               device="cpu")[0].numpy()
+        return (lambda: oracle.moe_topk_gating(lg, k, dtype="fp16")), nbytes, "full M=20480, E=128, k=2, fp16, numpy"
+
+    return dict(name="moe_topk_gating_ref_grid",
+                config={"workload": "moe_topk_gating", "M": M, "E": E, "k": k, "dtype": "fp16", "dist": "grid"},
+                metric="MoE gating HBM throughput", unit="GB/s", dtype="fp16", bound="hbm", bytes=nbytes,
+                flops=None, inputs=inputs, step=lambda x: impl_hip.run(*x), kernel="tb::gating_kernel<1, 32, 4, 2>",
+                cpu_sample=cpu_sample)
+
+
 def _w_fp8_quant():
     from tilebench_amd.data import tensors as T
     from tilebench_amd.benchmarks.operators.fp8_act_quant import impl_hip
@@ -287,6 +311,7 @@ WORKLOADS = {
     "int4_dequant": _w_int4_dequant,
     "moe_topk_gating_E64": _w_gating(64),
     "moe_topk_gating_E256": _w_gating(256),
+    "moe_topk_gating_ref_grid": _w_gating_reference_grid,
     "fp8_act_quant": _w_fp8_quant,
     "fp8_scaled_gemm": _w_fp8_gemm,
     "moe_w4a16_grouped_gemm": _w_grouped,

@@ -110,6 +110,28 @@ def test_gating_half_dtypes(gpu, dt):
     np.testing.assert_array_equal(ti.numpy(), ri)
 
 
+@pytest.mark.parametrize("M", [1024, 20480])
+@pytest.mark.parametrize("dt", ["fp16", "bf16", "fp32"])
+def test_gating_reference_grid(gpu, M, dt):
+    """The reference operator's own case grid (moe_topk_gating/config.yaml: E = 128,
+    k = 2, M = 1024..20480, fp16/bf16/fp32, distinct-value "grid" logits): indices
+    bit-exact, weights bit-exact in the half dtypes and within 1e-5 in fp32."""
+    from tilebench_amd.benchmarks.operators.moe_topk_gating import impl_hip
+
+    _say("gating reference grid", M, dt)
+    tdt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[dt]
+    logits, M, E, k = T.generate_moe_topk_gating_inputs(M, 128, 2, dtype=tdt, dist="grid", seed=M, device="cpu")
+    w, i = impl_hip.run(logits.to(gpu), M, E, k)
+    torch.cuda.synchronize()
+    bits = logits.view(torch.int16).numpy().view(np.uint16) if dt == "bf16" else logits.numpy()
+    rw, ri = oracle.moe_topk_gating(bits, k, dtype=dt)
+    np.testing.assert_array_equal(i.cpu().numpy(), ri)
+    if dt == "fp32":
+        np.testing.assert_allclose(w.cpu().numpy(), rw, atol=1e-5, rtol=1e-5)
+    else:
+        np.testing.assert_array_equal(_u16(w), np.asarray(rw).view(np.uint16))
+
+
 # ----------------------------------------------------------------------------- fp8 quant
 
 @pytest.mark.parametrize("M,K", [(8192, 8192), (64, 1024), (3, 24), (17, 2048 * 3), (5, 40000), (256, 16384)])

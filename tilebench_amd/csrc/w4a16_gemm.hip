@@ -10,24 +10,30 @@
 //
 //   A     : streamed HBM -> LDS by the buffer unit (buffer_load ... lds, no
 //           registers), three LDS stages, issued two steps ahead;
-//   W     : packed int4 tile prefetched two steps ahead into registers (each
-//           thread: 4 rows x 8 columns + its scales and zero-points), then
+//   W     : packed int4 tile of step k + 1 loaded into registers during step k
+//           (each thread: 4 rows x 8 columns + its scales and zero-points),
 //           dequantised once per block ((1024 + q) via the 0x6400 magic number,
 //           exact zero-point subtraction, one RNE multiply by the scale:
 //           bit-identical to the standalone dequantiser), transposed with byte
 //           permutes so each column holds consecutive k, and written to one of
-//           two LDS stages as W^T;
+//           two LDS stages as W^T.  The registers are consumed before the next
+//           loads are issued into them, so the wait that precedes the
+//           dequantisation only covers loads issued a full step earlier;
 //   LDS   : rows of 64 halfs in 16-byte chunks, chunk c of row r at slot
 //           c ^ ((r ^ (r >> 3)) & 7): the fragment reads (8 consecutive rows)
 //           and the W^T writes (rows 8 apart) are both free of bank conflicts;
-//   MFMA  : per k16 step a wavefront reads 4 A and 2 B fragments (one
-//           ds_read_b128 each) and issues 8 MFMAs;
+//   MFMA  : the fragments of k16 slice s + 1 are read while the 8 MFMAs of
+//           slice s run.  The MFMA computes the transposed product (W^T
+//           fragment as the first operand), so each lane ends with four
+//           consecutive output columns per accumulator group;
 //   order : every K step is split in two halves by a barrier.  The wavefronts
 //           of rows 0-127 run their MFMAs in the first half and dequantise in
 //           the second, those of rows 128-255 the other way round, so each
 //           SIMD always has one wavefront feeding its matrix pipe while the
-//           other keeps the vector ALU busy.
-//   output: the fp16 tile is staged in LDS and written with 16-byte row stores.
+//           other keeps the vector ALU busy; the wavefront in its MFMA phase
+//           runs at raised issue priority.
+//   output: the fp16 tile is staged in LDS with 8-byte writes and stored with
+//           16-byte row stores.
 //
 // Tiles are numbered XCD-aware: consecutive hardware block ids land on
 // different XCDs, so block ids are first regrouped so that each XCD owns a
@@ -217,78 +223,92 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
+  // The MFMA computes the transposed product (W^T fragment as the A operand,
+  // A fragment as the B operand): lane l then holds output row l % 32 and four
+  // consecutive output columns per group of four accumulator elements.
+  auto read_frags = [&](const _Float16* sa, const _Float16* sb, int ks, h8 (&fa)[4], h8 (&fb)[2]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[i] = *reinterpret_cast<const h8*>(sa + fa_base + i * 32 * 64 + fx[ks][i & 1]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) fb[j] = *reinterpret_cast<const h8*>(sb + fb_base + j * 32 * 64 + fx[ks][j & 1]);
+  };
   auto mfma_stage = [&](const _Float16* sa, const _Float16* sb) {
+    h8 fa[2][4], fb[2][2];
+    read_frags(sa, sb, 0, fa[0], fb[0]);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      h8 fa[4], fb[2];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) fa[i] = *reinterpret_cast<const h8*>(sa + fa_base + i * 32 * 64 + fx[ks][i & 1]);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) fb[j] = *reinterpret_cast<const h8*>(sb + fb_base + j * 32 * 64 + fx[ks][j & 1]);
+      const int cur = ks & 1;
+      // reads of slice ks + 1 go out before the MFMAs of slice ks, so their
+      // latency hides behind eight MFMAs
+      if (ks < 3) read_frags(sa, sb, ks + 1, fa[cur ^ 1], fb[cur ^ 1]);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[cur][j], fa[cur][i], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  constexpr int WAIT_VM10 = (10 & 15) | (7 << 4) | (15 << 8);
   constexpr int WAIT_VM0 = 0 | (7 << 4) | (15 << 8);
   const int nk = K / BK;
-  WRegs4 w0, w1;
+  WRegs4 wr;
   issue_a(0);
   if (nk > 1) issue_a(1);
-  issue_w(w0, 0);
-  if (nk > 1) issue_w(w1, 1);
-  dequant_store(w0, lds_b);
-  __builtin_amdgcn_s_waitcnt(0);
+  issue_w(wr, 0);
+  __builtin_amdgcn_s_waitcnt(WAIT_VM0);
+  dequant_store(wr, lds_b);
+  if (nk > 1) issue_w(wr, 1);
   __syncthreads();
 
-  auto step = [&](int kt, WRegs4& nxt, WRegs4& fill) {
-    const bool more = kt + 2 < nk;
-    if (more) {
+  // Step kt: MFMAs on A(kt), W(kt); dequantise W(kt + 1) (loaded one step
+  // earlier); then issue A(kt + 2) and W(kt + 2).  Consuming the registers
+  // before re-issuing into them keeps one W register set, and the wait before
+  // the dequantisation only covers loads issued a full step earlier.
+  auto dequant_and_issue = [&](int kt) {
+    if (kt + 1 < nk) {
+      __builtin_amdgcn_s_waitcnt(WAIT_VM0);
+      dequant_store(wr, lds_b + ((kt + 1) & 1) * B_STAGE);
+    }
+    if (kt + 2 < nk) {
       issue_a(kt + 2);
-      issue_w(fill, kt + 2);
+      issue_w(wr, kt + 2);
     }
-    // Two half-steps separated by a barrier: wave group 0 runs its MFMAs while
-    // group 1 dequantises, then the roles swap, so the MFMA pipe of every SIMD
-    // always has one wavefront feeding it.
-    if (wm == 1) {
-      if (kt + 1 < nk) dequant_store(nxt, lds_b + ((kt + 1) & 1) * B_STAGE);
-      __builtin_amdgcn_s_barrier();
-      mfma_stage(lds_a + (kt % A_STAGES) * A_STAGE, lds_b + (kt & 1) * B_STAGE);
-    } else {
-      mfma_stage(lds_a + (kt % A_STAGES) * A_STAGE, lds_b + (kt & 1) * B_STAGE);
-      __builtin_amdgcn_s_barrier();
-      if (kt + 1 < nk) dequant_store(nxt, lds_b + ((kt + 1) & 1) * B_STAGE);
-    }
-    // A tile kt+1 (DMA issued one step earlier) must have landed; the 10 loads
-    // issued in this step (4 DMA + 6 W) may stay in flight.
-    if (more) __builtin_amdgcn_s_waitcnt(WAIT_VM10);
-    else __builtin_amdgcn_s_waitcnt(WAIT_VM0);
-    __syncthreads();
   };
-  int kt = 0;
-  for (; kt + 1 < nk; kt += 2) {
-    step(kt, w1, w0);
-    step(kt + 1, w0, w1);
+  for (int kt = 0; kt < nk; ++kt) {
+    if (wm == 1) {
+      dequant_and_issue(kt);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_s_setprio(1);
+      mfma_stage(lds_a + (kt % A_STAGES) * A_STAGE, lds_b + (kt & 1) * B_STAGE);
+      __builtin_amdgcn_s_setprio(0);
+    } else {
+      __builtin_amdgcn_s_setprio(1);
+      mfma_stage(lds_a + (kt % A_STAGES) * A_STAGE, lds_b + (kt & 1) * B_STAGE);
+      __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_s_barrier();
+      dequant_and_issue(kt);
+    }
+    __syncthreads();
   }
-  if (kt < nk) step(kt, w1, w0);
 
   // Epilogue: stage the fp16 tile in LDS, then store 16-byte row chunks.
-  // Accumulator element e of fragment (i, j) is row i*32 + (e/4)*8 + (lane/32)*4 + e%4,
-  // column j*32 + lane%32 of the wave tile.
+  // Accumulator elements 4g .. 4g+3 of fragment (i, j) are row i*32 + lane%32,
+  // columns j*32 + g*8 + (lane/32)*4 + 0..3 of the wave tile.
   _Float16* ct = lds;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = wm * 128 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-        const int col = wn * 64 + j * 32 + (lane & 31);
-        ct[row * C_STRIDE + col] = (_Float16)acc[i][j][e];
+      for (int g = 0; g < 4; ++g) {
+        const int row = wm * 128 + i * 32 + (lane & 31);
+        const int col = wn * 64 + j * 32 + g * 8 + (lane >> 5) * 4;
+        u32x2v v;
+        v[0] = as_u32(f16x2{(_Float16)acc[i][j][4 * g], (_Float16)acc[i][j][4 * g + 1]});
+        v[1] = as_u32(f16x2{(_Float16)acc[i][j][4 * g + 2], (_Float16)acc[i][j][4 * g + 3]});
+        *reinterpret_cast<u32x2v*>(ct + row * C_STRIDE + col) = v;
       }
   __syncthreads();
   const int rows = min(BM, M - tile.m0);
