@@ -191,7 +191,7 @@ def _w4a16_check(gpu, M, K, N, G, seed):
 
 @pytest.mark.parametrize("M,K,N,G", [(1, 4096, 11008, 128), (16, 4096, 11008, 128), (256, 512, 512, 128),
                                      (300, 256, 264, 64), (7, 1024, 1000, 128), (16, 64, 8, 64), (1, 128, 2048, 128),
-                                     (512, 4096, 1024, 128), (33, 384, 392, 128)])
+                                     (512, 4096, 1024, 128), (33, 384, 392, 128), (5, 2048, 1032, 64)])
 def test_w4a16_gemm_matches_oracle(gpu, M, K, N, G):
     _w4a16_check(gpu, M, K, N, G, seed=M + N)
 

@@ -367,137 +367,181 @@ __global__ void __launch_bounds__(T4, 1)
 }
 
 // ---------------------------------------------------------------------------
-// Decode kernel (M <= 16, HBM-bound on the weights).  A block owns a 128-column
-// slab and one of S contiguous K ranges; its four wavefronts take the range's
-// 32-row units round-robin.  Per unit a lane loads an 8 x 8 int4 block (eight
-// 4-byte row loads, 16 lanes side by side cover 64 contiguous bytes of a row),
-// dequantises and transposes it exactly as the prefill kernel does, and feeds
-// eight v_mfma_f32_16x16x32_f16 (A rows >= M are zero): fragment j holds
-// columns 8c + j, c = lane % 16.  The four wave partials are summed in LDS in
+// Decode kernel (M <= 16, HBM-bound on the weights).  A block of eight
+// wavefronts owns a 256-column slab and one of S contiguous K ranges, and the
+// grid never holds more blocks than the device has CUs (one block fills a CU),
+// so every block starts at once.  Each wavefront streams its own contiguous
+// run of 32-row units with a four-unit prefetch; per unit a lane loads an
+// 8 x 16 int4 block (eight 8-byte row loads; 16 lanes side by side cover a
+// full 128-byte line of a row), dequantises it exactly as the prefill kernel
+// does, pairs consecutive rows of a column with one byte permute, and feeds
+// sixteen v_mfma_f32_16x16x32_f16 (A rows >= M are zero): fragment f holds
+// columns 16c + f, c = lane % 16.  The eight wave partials are summed in LDS in
 // a fixed order, so results are reproducible bit for bit.
 // Across the S blocks of a slab the reduction is a serial split-K: each block
-// stores its fp32 partial in the workspace, then bumps the slab's arrival
-// counter; the block that arrives last adds the S partials in slot order
-// (deterministic), writes fp16 Y and puts the counter back to zero, so the
-// workspace is ready for the next call without any clearing.
-constexpr int DEC_COLS = 128, DEC_THREADS = 256, DEC_UNIT = 32, DEC_PREFETCH = 4;
+// writes its fp32 partial through to the device-coherent level, then bumps the
+// slab's arrival counter; the block that arrives last reads the S partials
+// (all loads in flight at once), adds them in slot order (deterministic),
+// writes fp16 Y and puts the counter back to zero, so the workspace is ready
+// for the next call without any clearing.
+constexpr int DEC_COLS = 256, DEC_THREADS = 512, DEC_WAVES = 8, DEC_UNIT = 32, DEC_DEPTH = 4, DEC_MAX_SPLITS = 16;
+constexpr int AUX_SC1 = 16;  // buffer cache policy: coherent across the XCDs
 // Workspace layout, the same for every shape so that calls of different shapes
 // can share one buffer: [DEC_MAX_SLABS int32 arrival counters][fp32 partials].
 // Counters are left at zero by every call; partials never overlap them.
 constexpr int64_t DEC_MAX_SLABS = 4096;
 constexpr int64_t DEC_COUNTER_BYTES = DEC_MAX_SLABS * 4;
 
-typedef _Float16 h8d __attribute__((ext_vector_type(8)));
 typedef float f32x4d __attribute__((ext_vector_type(4)));
 
 struct DecUnit {
-  uint32_t w[8];
-  u32x4 a;
-  u32x4 s;
-  uint32_t z;
+  u32x2 w[8];  // rows kg*8 + r, columns 16c .. 16c + 15
+  u32x4 a;     // A row lane % 16, k = kg*8 .. +7
 };
 
 __global__ void __launch_bounds__(DEC_THREADS)
     w4a16_decode(const _Float16* __restrict__ A, const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
                  const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, float* __restrict__ partials,
                  int* __restrict__ counters, int M, int N, int K, int group, int splits) {
-  __shared__ float part[4][16 * DEC_COLS];  // one partial per wavefront, summed in fixed order
-  __shared__ float red[16 * DEC_COLS];
+  __shared__ float part[DEC_WAVES][16 * DEC_COLS];  // 128 KiB: one partial per wavefront
   __shared__ int last_flag;
   const int slab = blockIdx.x / splits, split = blockIdx.x % splits;
   const int n0 = slab * DEC_COLS;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 15, kg = lane >> 4;
-  const int n = n0 + c * 8;
-  const bool col_ok = n < N;
+  const int n = n0 + c * 16;
+  const bool col_ok = n < N;               // at least columns n .. n+7 exist (N % 8 == 0)
+  const bool col_full = n + 16 <= N;       // all 16 columns exist
   const int units = K / DEC_UNIT;
   const int u_begin = (int)((int64_t)units * split / splits), u_end = (int)((int64_t)units * (split + 1) / splits);
+  const int bu = u_end - u_begin;
+  const int w_begin = u_begin + (int)((int64_t)bu * wave / DEC_WAVES);
+  const int w_end = u_begin + (int)((int64_t)bu * (wave + 1) / DEC_WAVES);
   const int64_t half_n = N >> 1;
   const int arow = lane & 15;
 
-
-  f32x4d acc[8];
+  f32x4d acc[16];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] = f32x4d{};
+  for (int f = 0; f < 16; ++f) acc[f] = f32x4d{};
 
   auto load_unit = [&](DecUnit& d, int u) {
     const int k = u * DEC_UNIT + kg * 8;
+    const uint8_t* wp = W + (int64_t)k * half_n + (n >> 1);
 #pragma unroll
-    for (int r = 0; r < 8; ++r)
-      d.w[r] = col_ok ? __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(W + (int64_t)(k + r) * half_n + (n >> 1)))
-                      : 0u;
+    for (int r = 0; r < 8; ++r) {
+      const uint8_t* row = wp + (int64_t)r * half_n;
+      if (col_full) d.w[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(row));
+      else d.w[r] = u32x2{col_ok ? __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(row)) : 0u, 0u};
+    }
     d.a = arow < M ? *reinterpret_cast<const u32x4*>(A + (int64_t)arow * K + k) : u32x4{0u, 0u, 0u, 0u};
-    const int g = (u * DEC_UNIT) / group;
-    d.s = col_ok ? *reinterpret_cast<const u32x4*>(S + (int64_t)g * N + n) : u32x4{0u, 0u, 0u, 0u};
-    d.z = col_ok ? *reinterpret_cast<const uint32_t*>(Z + (int64_t)g * half_n + (n >> 1)) : 0u;
   };
-
-  for (int u0 = u_begin + wave; u0 < u_end; u0 += 4 * DEC_PREFETCH) {
-    DecUnit d[DEC_PREFETCH];
+  int cur_g = -1;
+  f16x2 zh[2][4], sh[2][4];
+  auto compute_unit = [&](const DecUnit& d, int u) {
+    const int g = (u * DEC_UNIT) / group;
+    if (g != cur_g) {
+      cur_g = g;
+      const _Float16* sp = S + (int64_t)g * N + n;
+      const uint8_t* zp = Z + (int64_t)g * half_n + (n >> 1);
+      const u32x4 s0 = col_ok ? *reinterpret_cast<const u32x4*>(sp) : u32x4{0u, 0u, 0u, 0u};
+      const u32x4 s1 = col_full ? *reinterpret_cast<const u32x4*>(sp + 8) : u32x4{0u, 0u, 0u, 0u};
+      const uint32_t z0 = col_ok ? *reinterpret_cast<const uint32_t*>(zp) : 0u;
+      const uint32_t z1 = col_full ? *reinterpret_cast<const uint32_t*>(zp + 4) : 0u;
+      unpack8(z0, zh[0]);
+      unpack8(z1, zh[1]);
 #pragma unroll
-    for (int p = 0; p < DEC_PREFETCH; ++p)
-      if (u0 + 4 * p < u_end) load_unit(d[p], u0 + 4 * p);
+      for (int j = 0; j < 4; ++j) {
+        sh[0][j] = as_h2(s0[j]);
+        sh[1][j] = as_h2(s1[j]);
+      }
+    }
+    const h8 af = __builtin_bit_cast(h8, d.a);
 #pragma unroll
-    for (int p = 0; p < DEC_PREFETCH; ++p) {
-      const int u = u0 + 4 * p;
-      if (u >= u_end) break;
-      f16x2 zh[4], sh[4];
-      unpack8(d[p].z, zh);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sh[j] = as_h2(d[p].s[j]);
+    for (int h = 0; h < 2; ++h) {
       uint32_t dq[8][4];
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
-        f16x2 h[4];
-        unpack8(d[p].w[r], h);
+        f16x2 hv[4];
+        unpack8(d.w[r][h], hv);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dq[r][j] = as_u32((h[j] - zh[j]) * sh[j]);
+        for (int j = 0; j < 4; ++j) dq[r][j] = as_u32((hv[j] - zh[h][j]) * sh[h][j]);
       }
-      const h8d af = __builtin_bit_cast(h8d, d[p].a);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const uint32_t sel = e ? 0x07060302u : 0x05040100u;
           u32x4 col;
 #pragma unroll
           for (int q = 0; q < 4; ++q) col[q] = perm(dq[2 * q + 1][j], dq[2 * q][j], sel);
-          acc[2 * j + e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, __builtin_bit_cast(h8d, col), acc[2 * j + e], 0, 0, 0);
+          const int f = h * 8 + 2 * j + e;
+          acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, __builtin_bit_cast(h8, col), acc[f], 0, 0, 0);
         }
+    }
+  };
+
+  DecUnit buf[DEC_DEPTH];
+#pragma unroll
+  for (int p = 0; p < DEC_DEPTH; ++p)
+    if (w_begin + p < w_end) load_unit(buf[p], w_begin + p);
+  for (int u = w_begin; u < w_end; u += DEC_DEPTH) {
+#pragma unroll
+    for (int p = 0; p < DEC_DEPTH; ++p) {
+      if (u + p < w_end) {
+        compute_unit(buf[p], u + p);
+        if (u + p + DEC_DEPTH < w_end) load_unit(buf[p], u + p + DEC_DEPTH);
       }
     }
   }
-  // Fragment j, element e: row 4 * (lane / 16) + e, column 8 * (lane % 16) + j.
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) part[wave][(4 * kg + e) * DEC_COLS + c * 8 + j] = acc[j][e];
-  __syncthreads();
-  for (int i = threadIdx.x; i < 16 * DEC_COLS; i += DEC_THREADS)
-    red[i] = ((part[0][i] + part[1][i]) + part[2][i]) + part[3][i];
-  __syncthreads();
 
+  // Accumulator f, element e: row 4 * (lane / 16) + e, column 16c + f.
+#pragma unroll
+  for (int f = 0; f < 16; ++f)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) part[wave][(4 * kg + e) * DEC_COLS + c * 16 + f] = acc[f][e];
+  __syncthreads();
+  // Fixed-order sum of the eight wave partials; thread t owns the float4 chunks
+  // t and t + 512 of the 16 x 256 tile.
   const int ncols = min(DEC_COLS, N - n0);
-  if (splits == 1) {
-    for (int i = threadIdx.x; i < M * DEC_COLS; i += DEC_THREADS) {
-      const int m = i / DEC_COLS, cc = i % DEC_COLS;
-      if (cc < ncols) Y[(int64_t)m * N + n0 + cc] = (_Float16)red[i];
+  constexpr int CH = 16 * DEC_COLS / 4 / DEC_THREADS;
+  f32x4d red[CH];
+#pragma unroll
+  for (int q = 0; q < CH; ++q) {
+    const int i = (threadIdx.x + q * DEC_THREADS) * 4;
+    f32x4d sum = *reinterpret_cast<const f32x4d*>(&part[0][i]);
+#pragma unroll
+    for (int w = 1; w < DEC_WAVES; ++w) sum += *reinterpret_cast<const f32x4d*>(&part[w][i]);
+    red[q] = sum;
+  }
+  auto store_y = [&](int q, f32x4d v) {
+    const int i = (threadIdx.x + q * DEC_THREADS) * 4;
+    const int m = i / DEC_COLS, cc = i % DEC_COLS;
+    if (m < M && cc < ncols) {  // ncols % 8 == 0, so a chunk is all in or all out
+      u32x2 h;
+      h[0] = as_u32(f16x2{(_Float16)v[0], (_Float16)v[1]});
+      h[1] = as_u32(f16x2{(_Float16)v[2], (_Float16)v[3]});
+      *reinterpret_cast<u32x2*>(Y + (int64_t)m * N + n0 + cc) = h;
     }
+  };
+  if (splits == 1) {
+#pragma unroll
+    for (int q = 0; q < CH; ++q) store_y(q, red[q]);
     return;
   }
-  // Serial split-K across the slab's blocks.  Every access to the partials and
-  // the counters is a device-scope atomic (coherent across the XCDs' L2s), so
-  // no cache-wide fence is needed: each thread waits until its partial stores
-  // are acknowledged (s_waitcnt 0) before the block's arrival is counted, and
-  // the last block reads the partials with device-scope loads.  (A release /
-  // acquire fence would write back and invalidate the whole L2 of the XCD in
-  // every block.)
-  float* mine = partials + ((int64_t)split * M) * N;
-  for (int i = threadIdx.x; i < M * DEC_COLS; i += DEC_THREADS) {
+  // Serial split-K across the slab's blocks.  Partials are written through to
+  // the device-coherent level (sc1) and read back the same way, so the last
+  // block sees every other block's partial without a cache-wide fence (which
+  // would write back and invalidate the whole L2 of the XCD in every block).
+  const rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(partials, 0, 0x7FFFFFFF, (int)RSRC_DW3);
+  auto poff = [&](int s2, int q) -> uint32_t {
+    const int i = (threadIdx.x + q * DEC_THREADS) * 4;
     const int m = i / DEC_COLS, cc = i % DEC_COLS;
-    if (cc < ncols) __hip_atomic_store(&mine[(int64_t)m * N + n0 + cc], red[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
+    return (m < M && cc < ncols) ? (uint32_t)((((int64_t)s2 * M + m) * N + n0 + cc) * 4) : OOB;
+  };
+#pragma unroll
+  for (int q = 0; q < CH; ++q)
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, red[q]), rp, poff(split, q), 0, AUX_SC1);
+  __builtin_amdgcn_s_waitcnt(0);  // partial stores acknowledged before the arrival is counted
   __syncthreads();
   if (threadIdx.x == 0) {
     const int prev = __hip_atomic_fetch_add(&counters[slab], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -505,25 +549,44 @@ __global__ void __launch_bounds__(DEC_THREADS)
   }
   __syncthreads();
   if (!last_flag) return;
-  for (int i = threadIdx.x; i < M * DEC_COLS; i += DEC_THREADS) {
-    const int m = i / DEC_COLS, cc = i % DEC_COLS;
-    if (cc >= ncols) continue;
-    float sum = 0.f;
-    for (int s2 = 0; s2 < splits; ++s2)
-      sum += s2 == split ? red[i]
-                         : __hip_atomic_load(&partials[((int64_t)s2 * M + m) * N + n0 + cc], __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-    Y[(int64_t)m * N + n0 + cc] = (_Float16)sum;
+  u32x4 v[CH][DEC_MAX_SPLITS];
+#pragma unroll
+  for (int q = 0; q < CH; ++q)
+#pragma unroll
+    for (int s2 = 0; s2 < DEC_MAX_SPLITS; ++s2)
+      if (s2 < splits && s2 != split) v[q][s2] = __builtin_amdgcn_raw_buffer_load_b128(rp, poff(s2, q), 0, AUX_SC1);
+#pragma unroll
+  for (int q = 0; q < CH; ++q) {
+    f32x4d sum = f32x4d{};
+#pragma unroll
+    for (int s2 = 0; s2 < DEC_MAX_SPLITS; ++s2)
+      if (s2 < splits) sum += s2 == split ? red[q] : __builtin_bit_cast(f32x4d, v[q][s2]);
+    store_y(q, sum);
   }
   if (threadIdx.x == 0) __hip_atomic_store(&counters[slab], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Number of CUs of the current device, cached per device.
+inline int device_cus() {
+  static int cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cache[dev] = cus;
+  }
+  return cache[dev];
+}
+
+// One block per CU: slabs x splits never exceeds the CU count.
 inline int decode_splits(int N, int K) {
   const int slabs = (N + DEC_COLS - 1) / DEC_COLS;
   const int units = K / DEC_UNIT;
-  int s = (512 + slabs - 1) / slabs;  // aim at ~2 blocks per CU
-  s = std::max(1, std::min(s, units / 4));
-  return s;
+  int s = device_cus() / slabs;
+  s = std::min(s, DEC_MAX_SPLITS);
+  s = std::min(s, units / DEC_WAVES);
+  return std::max(s, 1);
 }
 
 }  // namespace w4a16
