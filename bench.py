@@ -32,9 +32,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
-# MI355X published peaks (dense): HBM3E 8 TB/s; MFMA fp16/bf16 2.5 PFLOP/s, fp8 5.0 PFLOP/s.
+# MI355X published peaks (dense): HBM3E 8 TB/s; MFMA fp16/bf16 2.5 PFLOP/s, fp8 5.0 PFLOP/s,
+# int8 5.0 POP/s, fp32 157.3 TFLOP/s.
 PEAK_HBM_GBS = 8000.0
-PEAK_TFLOPS = {"fp16": 2500.0, "bf16": 2500.0, "fp8": 5000.0}
+PEAK_TFLOPS = {"fp16": 2500.0, "bf16": 2500.0, "fp8": 5000.0, "int8": 5000.0, "fp32": 157.3}
 
 
 # ----------------------------------------------------------------------------- workloads
@@ -284,6 +285,70 @@ def _w_quantize_global():
                 cpu_sample=cpu_sample)
 
 
+def _w_matmul_int8():
+    from tilebench_amd.data import tensors as T
+    from tilebench_amd.benchmarks.operators.matmul_int8 import impl_hip
+
+    M = N = 2048
+    K = 20480
+    nbytes = M * K + K * N // 4 + 4 * M * N          # matmul_int8/config.yaml bytes_expr
+
+    def inputs():
+        return T.generate_matmul_int8_inputs(M, N, K, seed=13, device="cuda")
+
+    def cpu_sample():
+        import oracle
+        rows = 256
+        a, b = T.generate_matmul_int8_inputs(M, N, K, seed=13, device="cpu")
+        a, b = a.numpy()[:rows], b.numpy()
+        return (lambda: oracle.matmul_int8(a, b)), 2 * rows * N * K, f"{rows} of {M} rows, numpy float64 BLAS (exact)"
+
+    return dict(name="matmul_int8", config={"workload": "matmul_int8", "M": M, "N": N, "K": K},
+                metric="matmul_int8 throughput", unit="TFLOP/s", dtype="int8 x int2 -> int32", bound="mfma",
+                peak_key="int8", bytes=nbytes, flops=2 * M * N * K, inputs=inputs, step=lambda x: impl_hip.run(*x),
+                kernel="tb::ntg::nt_gemm<3, 4, 128, 128, 64, 64>", cpu_sample=cpu_sample)
+
+
+def _w_matmul(dt):
+    def make():
+        import torch
+        from tilebench_amd.data import tensors as T
+        from tilebench_amd.benchmarks.operators.matmul_fp32_fp16_fp8 import impl_hip
+
+        M = N = 4096
+        K = 20480
+        tdt = {"fp32": torch.float32, "fp16": torch.float16, "fp8_e4m3fn": torch.float8_e4m3fn}[dt]
+        esz = {"fp32": 4, "fp16": 2, "fp8_e4m3fn": 1}[dt]
+        nbytes = (M * K + K * N + M * N) * esz          # matmul_fp32_fp16_fp8/config.yaml bytes_expr
+
+        def inputs():
+            return T.generate_matmul_fp32_fp16_fp8_inputs(M, N, K, dtype=tdt, seed=14, device="cuda")
+
+        def cpu_sample():
+            import oracle
+            rows = 64
+            a, b = T.generate_matmul_fp32_fp16_fp8_inputs(M, N, K, dtype=tdt, seed=14, device="cpu")
+            if dt == "fp8_e4m3fn":
+                a8, b8 = a.view(torch.uint8).numpy()[:rows], b.view(torch.uint8).numpy()
+                fn = lambda: oracle.matmul_fp8(a8, b8)
+            elif dt == "fp16":
+                a16, b16 = a.numpy()[:rows], b.numpy()
+                fn = lambda: oracle.matmul_f16(a16, b16)
+            else:
+                a32, b32 = a.numpy()[:rows], b.numpy()
+                fn = lambda: oracle.matmul_f32(a32, b32)
+            return fn, 2 * rows * N * K, f"{rows} of {M} rows, numpy float64 BLAS"
+
+        kern = {"fp32": "tb::ntg::nt_gemm<2, 3, 256, 256, 128, 64>", "fp16": "tb::ntg::nt_gemm<1, 2, 256, 256, 128, 64>",
+                "fp8_e4m3fn": "tb::ntg::nt_gemm<0, 1, 256, 256, 128, 64>"}[dt]
+        peak = {"fp32": "fp32", "fp16": "fp16", "fp8_e4m3fn": "fp8"}[dt]
+        return dict(name=f"matmul_{dt}", config={"workload": "matmul_fp32_fp16_fp8", "M": M, "N": N, "K": K, "dtype": dt},
+                    metric="matmul throughput", unit="TFLOP/s", dtype=dt if dt != "fp32" else "fp32 (3 x bf16 products)",
+                    bound="mfma", peak_key=peak, bytes=nbytes, flops=2 * M * N * K, inputs=inputs,
+                    step=lambda x: impl_hip.run(*x), kernel=kern, cpu_sample=cpu_sample)
+    return make
+
+
 def _w_copy():
     import torch
 
@@ -318,6 +383,10 @@ WORKLOADS = {
     "weight_dequant": _w_weight_dequant,
     "dequantize_rowwise": _w_dequantize_rowwise,
     "quantize_global": _w_quantize_global,
+    "matmul_int8": _w_matmul_int8,
+    "matmul_fp16": _w_matmul("fp16"),
+    "matmul_fp8": _w_matmul("fp8_e4m3fn"),
+    "matmul_fp32": _w_matmul("fp32"),
     "hbm_copy_probe": _w_copy,
 }
 DEFAULT_OP = "w4a16_gemm_M4096"

@@ -165,6 +165,36 @@ tb_status tb_dequantize_rowwise(const int8_t* x, const float* state, uint16_t* y
 tb_status tb_quantize_global(const float* x, uint16_t* y, int64_t n, hipStream_t stream);
 
 /*
+ * The reference's plain GEMM operators (MFMA "NT" GEMM; the second operand is
+ * first transposed, unpacked or split into the caller's workspace).
+ *
+ * tb_matmul_int8: out int32 [M, N] = a int8 [M, K] @ B, where b uint8 [K/4, N]
+ *   holds four 2-bit fields per byte and row i*K/4 + kb of B is
+ *   ((b[kb, :] >> 2i) & 3) - 1.  Exact integer arithmetic.  Needs K % 128 == 0,
+ *   N % 8 == 0 and a workspace of tb_matmul_workspace_size(3, ...) bytes.
+ *   Replaces: matmul_int8/impl_triton.py:118 run(a, b) (semantics impl_torch.py:4-19).
+ * tb_matmul: dtype 0 fp32, 1 fp16, 2 fp8-e4m3; a [M, K], b [K, N] and out
+ *   [M, N] of that dtype.  fp16: fp16(a @ b) with fp32 accumulation.  fp8:
+ *   e4m3(bf16(a @ b)) (the reference's unit-scale _scaled_mm to bf16, then its
+ *   cast back to e4m3, RNE, no saturation).  fp32: fp32 accumulation of three
+ *   bf16 products per term (hi*hi + hi*lo + lo*hi, about 2^-16 relative per
+ *   product).  Needs K a multiple of 128 bytes of the dtype (fp32: of 64),
+ *   N % 8 == 0 and a workspace of tb_matmul_workspace_size(dtype, ...) bytes.
+ *   Replaces: matmul_fp32_fp16_fp8/impl_triton.py:124 run(a, b) (semantics impl_torch.py:21-27).
+ * tb_matmul_fp8_bt: the fp8 case with b already transposed to bT [N, K] (the
+ *   column-major copy impl_torch.py:10-18 caches per operand pair), no workspace.
+ * tb_matmul_workspace_size: workspace bytes for tb_matmul (dtype 0-2) or
+ *   tb_matmul_int8 (dtype 3).
+ */
+tb_status tb_matmul_int8(const int8_t* a, const uint8_t* b, int32_t* out, int64_t M, int64_t N, int64_t K,
+                         void* workspace, int64_t workspace_bytes, hipStream_t stream);
+tb_status tb_matmul(int dtype, const void* a, const void* b, void* out, int64_t M, int64_t N, int64_t K,
+                    void* workspace, int64_t workspace_bytes, hipStream_t stream);
+tb_status tb_matmul_fp8_bt(const uint8_t* a, const uint8_t* bT, uint8_t* out, int64_t M, int64_t N, int64_t K,
+                           hipStream_t stream);
+tb_status tb_matmul_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int64_t* bytes);
+
+/*
  * Fill `bytes` bytes of `buf` with a 32-bit pattern using a plain store
  * kernel.  Used to evict the L2 and the 256 MiB MALL between timed launches
  * (a kernel, not hipMemset, so it may be captured into a graph).

@@ -24,6 +24,9 @@ BASELINE config text):
 * weight_dequant    — weight_dequant/impl_torch.py:4-8; dequantize_rowwise —
                       dequantize_rowwise/impl_torch.py:4-7; quantize_global —
                       quantize_global/impl_torch.py:4-5 (the reference's own operators).
+* matmul_int8       — matmul_int8/impl_torch.py:4-19 (2-bit unpack, value - 1, exact).
+* matmul_*          — matmul_fp32_fp16_fp8/impl_torch.py:21-27 (matmul; fp8 through
+                      a unit-scale _scaled_mm to bf16 and a cast back to e4m3).
 
 How each function is pinned (tests/test_oracle.py): closed forms and exact
 rational arithmetic (dequant), the torch CPU fp8 cast over every fp16 value and
@@ -47,4 +50,9 @@ from .core import (  # noqa: F401
     weight_dequant,
     dequantize_rowwise,
     quantize_global,
+    unpack_i2,
+    matmul_int8,
+    matmul_f16,
+    matmul_f32,
+    matmul_fp8,
 )

@@ -243,3 +243,46 @@ def quantize_global(x: np.ndarray) -> np.ndarray:
     """fp32 -> fp16, round to nearest even (overflow -> inf)."""
     with np.errstate(over="ignore"):
         return np.asarray(x, np.float32).astype(np.float16)
+
+
+# ----------------------------------------------------------------------------- plain GEMM operators
+
+
+def unpack_i2(b: np.ndarray, K: int) -> np.ndarray:
+    """uint8 [K/4, N] with four 2-bit fields per byte -> int8 [K, N]: row
+    i*K/4 + kb is ((b[kb] >> 2i) & 3) - 1 (matmul_int8/impl_torch.py:10-14)."""
+    b = np.asarray(b, dtype=np.uint8)
+    Kb = b.shape[0]
+    if K != 4 * Kb:
+        raise ValueError("A's K dim must be 4x B's K_b dim")
+    return np.concatenate([((b >> (2 * i)) & 3).astype(np.int8) - 1 for i in range(4)], axis=0)
+
+
+def matmul_int8(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """int32 [M, N] = a int8 [M, K] @ unpack_i2(b), exact (matmul_int8/impl_torch.py:4-19,
+    whose fp32 matmul is exact for these ranges: |sum| < 2^24)."""
+    a = np.asarray(a, dtype=np.int8)
+    B = unpack_i2(b, a.shape[1])
+    # every partial sum is an integer below 2^53 in magnitude, so float64 BLAS is exact
+    return np.rint(a.astype(np.float64) @ B.astype(np.float64)).astype(np.int64).astype(np.int32)
+
+
+def matmul_f16(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """fp16 [M, N] = fp16(a @ b), products and sum in float64 (the reference's
+    fp32-accumulated torch.matmul differs from it by accumulation rounding only)."""
+    return (np.asarray(a, np.float16).astype(np.float64) @ np.asarray(b, np.float16).astype(np.float64)).astype(np.float16)
+
+
+def matmul_f32(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """fp32 [M, N] = a @ b in float64, rounded once."""
+    return (np.asarray(a, np.float32).astype(np.float64) @ np.asarray(b, np.float32).astype(np.float64)).astype(np.float32)
+
+
+def matmul_fp8(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """e4m3 codes [M, N] = e4m3(bf16(a @ b)) for e4m3 code operands a [M, K],
+    b [K, N]: the reference's _scaled_mm with unit scales and bf16 output, then
+    .to(float8_e4m3fn) (matmul_fp32_fp16_fp8/impl_torch.py:21-26).  Products of
+    e4m3 values are exact in float64."""
+    acc = e4m3_to_f32(a).astype(np.float64) @ e4m3_to_f32(b).astype(np.float64)
+    y16 = bf16_bits_to_f32(f32_to_bf16_bits(acc.astype(np.float32)))
+    return e4m3_from_f32(y16)

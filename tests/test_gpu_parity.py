@@ -422,3 +422,73 @@ def test_quantize_global_matches_oracle(gpu, n):
     y = impl_hip.run(x.to(gpu))
     torch.cuda.synchronize()
     np.testing.assert_array_equal(_u16(y), oracle.quantize_global(x.numpy()).view(np.uint16))
+
+
+# ----------------------------------------------------------------------------- plain GEMM operators
+
+def _rows(M, n, seed):
+    return np.sort(np.random.default_rng(seed).choice(M, min(M, n), replace=False))
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 1024), (100, 264, 512), (2048, 2048, 1024), (2048, 2048, 20480),
+                                   (1024, 1024, 128), (4096, 4096, 1024)])
+def test_matmul_int8_bit_exact(gpu, M, N, K):
+    from tilebench_amd.benchmarks.operators.matmul_int8 import impl_hip
+
+    _say("matmul_int8", M, N, K)
+    a, b = T.generate_matmul_int8_inputs(M, N, K, seed=M + K, device="cpu")
+    out = impl_hip.run(a.to(gpu), b.to(gpu))
+    torch.cuda.synchronize()
+    rows = _rows(M, 128, K)
+    np.testing.assert_array_equal(out.cpu().numpy()[rows], oracle.matmul_int8(a.numpy()[rows], b.numpy()))
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 512, 1024), (300, 136, 256), (4096, 4096, 4096)])
+def test_matmul_fp16(gpu, M, N, K):
+    from tilebench_amd.benchmarks.operators.matmul_fp32_fp16_fp8 import impl_hip
+
+    _say("matmul fp16", M, N, K)
+    a, b = T.generate_matmul_fp32_fp16_fp8_inputs(M, N, K, dtype=torch.float16, seed=M + K, device="cpu")
+    out = impl_hip.run(a.to(gpu), b.to(gpu))
+    torch.cuda.synchronize()
+    rows = _rows(M, 128, K)
+    ref = oracle.matmul_f16(a.numpy()[rows], b.numpy()).astype(np.float32)
+    np.testing.assert_allclose(out.cpu().numpy()[rows].astype(np.float32), ref, atol=2e-3, rtol=2e-3)
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 512, 1024), (300, 136, 64), (4096, 4096, 2048)])
+def test_matmul_fp32_three_bf16_products(gpu, M, N, K):
+    """fp32 operands through hi/lo bf16 splits: within 1e-4 of the float64 product,
+    an order of magnitude tighter than TF32 (10 mantissa bits) would allow."""
+    from tilebench_amd.benchmarks.operators.matmul_fp32_fp16_fp8 import impl_hip
+
+    _say("matmul fp32", M, N, K)
+    a, b = T.generate_matmul_fp32_fp16_fp8_inputs(M, N, K, dtype=torch.float32, seed=M + K, device="cpu")
+    out = impl_hip.run(a.to(gpu), b.to(gpu))
+    torch.cuda.synchronize()
+    rows = _rows(M, 128, K)
+    ref = oracle.matmul_f32(a.numpy()[rows], b.numpy())
+    np.testing.assert_allclose(out.cpu().numpy()[rows], ref, atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 512, 1024), (300, 136, 128), (4096, 4096, 4096)])
+def test_matmul_fp8(gpu, M, N, K):
+    """e4m3(bf16(a @ b)): fp32 accumulation against the oracle's float64 may move a
+    bf16 rounding on rare values, so codes agree exactly on > 99.5 % and the
+    decoded values never differ by more than one e4m3 step."""
+    from tilebench_amd.benchmarks.operators.matmul_fp32_fp16_fp8 import impl_hip
+
+    _say("matmul fp8", M, N, K)
+    a, b = T.generate_matmul_fp32_fp16_fp8_inputs(M, N, K, dtype=torch.float8_e4m3fn, seed=M + K, device="cpu")
+    ag, bg = a.to(gpu), b.to(gpu)
+    out = impl_hip.run(ag, bg)
+    out2 = impl_hip.run(ag, bg)   # second call: cached transposed operand
+    torch.cuda.synchronize()
+    rows = _rows(M, 128, K)
+    got = out.cpu().view(torch.uint8).numpy()[rows]
+    ref = oracle.matmul_fp8(a.view(torch.uint8).numpy()[rows], b.view(torch.uint8).numpy())
+    assert (got == ref).mean() > 0.995
+    g, r = oracle.e4m3_to_f32(got), oracle.e4m3_to_f32(ref)
+    step = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(r), 2.0 ** -6))) - 3)
+    assert (np.abs(g - r) <= step + 1e-12).all()
+    assert torch.equal(out.view(torch.uint8), out2.view(torch.uint8))

@@ -1,0 +1,44 @@
+"""hip backend of matmul_fp32_fp16_fp8: tb_matmul / tb_matmul_fp8_bt in libtbhip.so.
+
+fp16: fp16 MFMA, fp32 accumulation.  fp8-e4m3: fp8 MFMA, fp32 accumulation,
+bf16 then e4m3 rounding, with the column-major copy of b cached per operand
+pair as the reference does (impl_torch.py:10-18).  fp32: three bf16 products
+per term on the bf16 matrix cores (about 2^-16 relative per product, finer
+than the TF32 the reference enables)."""
+import torch
+
+from tilebench_amd import runtime as rt
+
+rt.load_library()
+
+_DT = {torch.float32: 0, torch.float16: 1, torch.float8_e4m3fn: 2}
+_bt_cache: dict = {}
+
+
+def run(a: torch.Tensor, b: torch.Tensor, **kwargs):
+    rt.require_device()
+    if a.dtype not in _DT or b.dtype != a.dtype:
+        raise TypeError(f"matmul_fp32_fp16_fp8: unsupported dtypes {a.dtype} / {b.dtype}")
+    a = a.contiguous()
+    M, K = a.shape
+    N = b.shape[1]
+    dt = _DT[a.dtype]
+    out = torch.empty((M, N), dtype=a.dtype, device=a.device)
+    stream = rt.stream_handle(a.device)
+    if dt == 2:
+        key = (a.data_ptr(), b.data_ptr(), tuple(a.shape), tuple(b.shape))
+        bT = _bt_cache.get(key)
+        if bT is None:
+            bT = b.t().contiguous()
+            _bt_cache[key] = bT
+        rt.call("tb_matmul_fp8_bt", a.data_ptr(), bT.data_ptr(), out.data_ptr(), M, N, K, stream)
+        return out
+    b = b.contiguous()
+    need = rt.matmul_workspace_size(dt, M, N, K)
+    ws = torch.empty(need, dtype=torch.uint8, device=a.device)
+    rt.call("tb_matmul", dt, a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, ws.data_ptr(), need, stream)
+    return out
+
+
+def get_last_config():
+    return {"kernel": "nt_gemm", "tile": "256x256"}

@@ -1,0 +1,28 @@
+"""hip backend of matmul_int8: tb_matmul_int8 in libtbhip.so (2-bit unpack into
+a transposed int8 operand, then the int8 MFMA GEMM; exact int32 result)."""
+import torch
+
+from tilebench_amd import runtime as rt
+
+rt.load_library()
+
+
+def run(a: torch.Tensor, b: torch.Tensor, **kwargs):
+    rt.require_device()
+    if a.dtype != torch.int8 or b.dtype != torch.uint8:
+        raise TypeError("matmul_int8 expects int8 a and uint8 b")
+    a, b = a.contiguous(), b.contiguous()
+    M, K = a.shape
+    N = b.shape[1]
+    if K != 4 * b.shape[0]:
+        raise ValueError("A's K dim must be 4x B's K_b dim")
+    out = torch.empty((M, N), dtype=torch.int32, device=a.device)
+    need = rt.matmul_workspace_size(3, M, N, K)
+    ws = torch.empty(need, dtype=torch.uint8, device=a.device)
+    rt.call("tb_matmul_int8", a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, ws.data_ptr(), need,
+            rt.stream_handle(a.device))
+    return out
+
+
+def get_last_config():
+    return {"kernel": "nt_gemm<i8>", "tile": "128x128"}

@@ -35,22 +35,6 @@
 
 namespace tb {
 
-__device__ __forceinline__ uint32_t e4m3_code(float q) {
-  uint32_t b = __builtin_bit_cast(uint32_t, q);
-  const uint32_t sign = (b >> 24) & 0x80u;
-  b &= 0x7FFFFFFFu;
-  uint32_t c;
-  if (b >= 0x43F00000u) {
-    c = 0x7Fu;
-  } else if (b < (121u << 23)) {
-    const float t = __builtin_bit_cast(float, b) + 16384.0f;
-    c = __builtin_bit_cast(uint32_t, t) - (141u << 23);
-  } else {
-    c = (b + 0xC407FFFFu + ((b >> 20) & 1u)) >> 20;  // 0xC407FFFF = (-120 << 23) + 0x7FFFF (mod 2^32)
-  }
-  return (c | sign) & 0xFFu;
-}
-
 // The refinement yields +0 for x = -0 (fma(+0, y, -0) = +0); sa and y are
 // positive, so the quotient always carries the sign of x and copysign restores it.
 __device__ __forceinline__ float quotient(float x, float sa, float y) {

@@ -69,4 +69,32 @@ __device__ __forceinline__ uint32_t as_u32(f16x2 v) { return __builtin_bit_cast(
 // into the mantissa is an exact conversion.
 __device__ __forceinline__ f16x2 magic_h2(uint32_t pair) { return as_h2(pair | 0x64006400u); }
 
+// fp32 -> OCP fp8-e4m3 code, round to nearest even, no saturation: magnitudes
+// at or above 480 (whose rounding would need the reserved S.1111.111 pattern),
+// inf and NaN give the NaN code 0x7F with the sign kept, as torch's
+// float -> float8_e4m3fn cast does.  Subnormals (below 2^-6) round onto the
+// 2^-9 grid through one fp32 addition of 2^14, whose ulp is 2^-9.
+__device__ __forceinline__ uint32_t e4m3_code(float q) {
+  uint32_t b = __builtin_bit_cast(uint32_t, q);
+  const uint32_t sign = (b >> 24) & 0x80u;
+  b &= 0x7FFFFFFFu;
+  uint32_t c;
+  if (b >= 0x43F00000u) {
+    c = 0x7Fu;
+  } else if (b < (121u << 23)) {
+    const float t = __builtin_bit_cast(float, b) + 16384.0f;
+    c = __builtin_bit_cast(uint32_t, t) - (141u << 23);
+  } else {
+    c = (b + 0xC407FFFFu + ((b >> 20) & 1u)) >> 20;  // 0xC407FFFF = (-120 << 23) + 0x7FFFF (mod 2^32)
+  }
+  return (c | sign) & 0xFFu;
+}
+
+// fp32 -> bf16 bits, round to nearest even, NaN kept quiet.
+__device__ __forceinline__ uint32_t bf16_bits(float f) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, f);
+  if ((b & 0x7FFFFFFFu) > 0x7F800000u) return (b >> 16) | 0x40u;
+  return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+
 }  // namespace tb

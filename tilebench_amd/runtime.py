@@ -42,6 +42,10 @@ SIGNATURES: dict[str, list] = {
     "tb_weight_dequant": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p],
     "tb_dequantize_rowwise": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_p],
     "tb_quantize_global": [_c_p, _c_p, _c_i64, _c_p],
+    "tb_matmul_int8": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p],
+    "tb_matmul": [_c_int, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p],
+    "tb_matmul_fp8_bt": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p],
+    "tb_matmul_workspace_size": [_c_int, _c_i64, _c_i64, _c_i64, ctypes.POINTER(_c_i64)],
     "tb_l2_flush": [_c_p, _c_i64, _c_u32, _c_p],
     "tb_probe_copy": [_c_p, _c_p, _c_i64, _c_p],
     "tb_probe_mfma": [_c_int, _c_i64, _c_i64, _c_p, _c_p],
@@ -131,6 +135,14 @@ def ptr(t) -> int:
 
 
 _workspaces: dict = {}
+
+
+def matmul_workspace_size(dtype: int, M: int, N: int, K: int) -> int:
+    """Bytes of workspace tb_matmul (dtype 0 fp32, 1 fp16, 2 fp8) or
+    tb_matmul_int8 (dtype 3) needs for this shape."""
+    out = ctypes.c_int64(0)
+    call("tb_matmul_workspace_size", dtype, M, N, K, ctypes.byref(out))
+    return int(out.value)
 
 
 def workspace(nbytes: int, device, stream: int):
