@@ -310,96 +310,149 @@ __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64, 1)
 
 // ------------------------------------------------------------------ preparation passes
 
-// B [K, N] (E bytes per element) -> B^T [N, K]: 64 x 64 element tiles through LDS.
+// The preparation passes move 64 x 64 element tiles through LDS with 16-byte
+// global loads along the source rows and 16-byte global stores along the
+// destination rows (consecutive threads take consecutive chunks of one
+// destination row, so each row segment is written by one coalesced group).
+
+// B [K, N] (E = 1 or 2 bytes per element) -> B^T [N, K].  Needs N % 8 == 0 and
+// K a multiple of 16 / E; partial source chunks at the N edge fall back to
+// element loads.
 template <int E>
 __global__ void __launch_bounds__(256) transpose_tile(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
                                                       int K, int N) {
-  __shared__ uint8_t tile[64][64 * E + 4];
-  const int k0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  constexpr int T = 64, V = 16 / E;  // elements per 16-byte chunk
+  constexpr int ROW = T * E + 16;    // padded LDS row (bytes), 16-byte aligned
+  __shared__ __attribute__((aligned(16))) uint8_t tile[T * ROW];
+  const int k0 = blockIdx.y * T, n0 = blockIdx.x * T;
   const int t = threadIdx.x;
-  for (int idx = t; idx < 64 * 64; idx += 256) {
-    const int r = idx >> 6, c = idx & 63;
-    const int k = k0 + r, n = n0 + c;
+  for (int idx = t; idx < T * (T / V); idx += 256) {
+    const int r = idx / (T / V), c = idx % (T / V);
+    const int k = k0 + r, n = n0 + c * V;
+    u32x4 v = {0u, 0u, 0u, 0u};
     if (k < K && n < N) {
-#pragma unroll
-      for (int b = 0; b < E; ++b) tile[r][c * E + b] = src[((int64_t)k * N + n) * E + b];
+      const uint8_t* p = src + ((int64_t)k * N + n) * E;
+      if (n + V <= N && ((N * E) & 15) == 0) {  // 16-byte aligned rows
+        v = *reinterpret_cast<const u32x4*>(p);
+      } else {
+        uint8_t b[16] = {};
+        for (int q = 0; q < min(V, N - n) * E; ++q) b[q] = p[q];
+        v = __builtin_bit_cast(u32x4, b);
+      }
     }
+    *reinterpret_cast<u32x4*>(tile + r * ROW + c * 16) = v;
   }
   __syncthreads();
-  for (int idx = t; idx < 64 * 64; idx += 256) {
-    const int r = idx >> 6, c = idx & 63;  // r: n, c: k
-    const int n = n0 + r, k = k0 + c;
-    if (k < K && n < N) {
+  for (int idx = t; idx < T * (T / V); idx += 256) {
+    const int r = idx / (T / V), c = idx % (T / V);  // r: n, c: chunk of k
+    const int n = n0 + r, k = k0 + c * V;
+    if (n >= N || k >= K) continue;
+    uint8_t b[16];
 #pragma unroll
-      for (int b = 0; b < E; ++b) dst[((int64_t)n * K + k) * E + b] = tile[c][r * E + b];
-    }
+    for (int q = 0; q < V; ++q)
+#pragma unroll
+      for (int e = 0; e < E; ++e) b[q * E + e] = tile[(c * V + q) * ROW + r * E + e];
+    *reinterpret_cast<u32x4*>(dst + ((int64_t)n * K + k) * E) = __builtin_bit_cast(u32x4, b);
   }
 }
 
 // int8 unpack + transpose: packed [K/4, N] -> B^T int8 [N, K] with
-// B^T[n, i*K/4 + kb] = ((packed[kb, n] >> 2i) & 3) - 1.
+// B^T[n, i*K/4 + kb] = ((packed[kb, n] >> 2i) & 3) - 1.  Needs K/4 % 16 == 0.
 __global__ void __launch_bounds__(256) unpack_i2_tile(const uint8_t* __restrict__ packed, int8_t* __restrict__ dst,
                                                       int K, int N) {
-  __shared__ uint8_t tile[64][65];
+  constexpr int T = 64, ROW = T + 16;
+  __shared__ __attribute__((aligned(16))) uint8_t tile[T * ROW];
   const int Kb = K / 4;
-  const int kb0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  const int kb0 = blockIdx.y * T, n0 = blockIdx.x * T;
   const int t = threadIdx.x;
-  for (int idx = t; idx < 64 * 64; idx += 256) {
-    const int r = idx >> 6, c = idx & 63;
-    const int kb = kb0 + r, n = n0 + c;
-    tile[r][c] = (kb < Kb && n < N) ? packed[(int64_t)kb * N + n] : 0;
+  for (int idx = t; idx < T * (T / 16); idx += 256) {
+    const int r = idx / (T / 16), c = idx % (T / 16);
+    const int kb = kb0 + r, n = n0 + c * 16;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (kb < Kb && n < N) {
+      const uint8_t* p = packed + (int64_t)kb * N + n;
+      if (n + 16 <= N && (N & 15) == 0) {  // 16-byte aligned rows
+        v = *reinterpret_cast<const u32x4*>(p);
+      } else {
+        uint8_t b[16] = {};
+        for (int q = 0; q < min(16, N - n); ++q) b[q] = p[q];
+        v = __builtin_bit_cast(u32x4, b);
+      }
+    }
+    *reinterpret_cast<u32x4*>(tile + r * ROW + c * 16) = v;
   }
   __syncthreads();
-  for (int idx = t; idx < 4 * 64 * 64; idx += 256) {
-    const int i = idx >> 12, rem = idx & 4095;
-    const int r = rem >> 6, c = rem & 63;  // r: n, c: kb
-    const int n = n0 + r, kb = kb0 + c;
-    if (kb < Kb && n < N) dst[(int64_t)n * K + i * Kb + kb] = (int8_t)(((tile[c][r] >> (2 * i)) & 3) - 1);
+  // output chunk: row n, quarter i, 16 consecutive kb
+  for (int idx = t; idx < T * 4 * (T / 16); idx += 256) {
+    const int c = idx % (T / 16), i = (idx / (T / 16)) % 4, r = idx / (4 * (T / 16));
+    const int n = n0 + r, kb = kb0 + c * 16;
+    if (n >= N || kb >= Kb) continue;
+    uint32_t w[4];
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      uint32_t x = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) x |= (uint32_t)tile[(c * 16 + q4 * 4 + q) * ROW + r] << (8 * q);
+      // field i of four bytes at once, minus one per byte without carries: (f + 0x7F) ^ 0x80 = f - 1
+      w[q4] = (((x >> (2 * i)) & 0x03030303u) + 0x7F7F7F7Fu) ^ 0x80808080u;
+    }
+    *reinterpret_cast<u32x4*>(dst + (int64_t)n * K + i * Kb + kb) = u32x4{w[0], w[1], w[2], w[3]};
   }
 }
 
 // fp32 split for the three-product bf16 GEMM.  A [M, K] -> A' [M, 3K] =
 // [hi | hi | lo]; B [K, N] -> B'^T [N, 3K] = [hi^T | lo^T | hi^T].
-__device__ __forceinline__ void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
-  hi = (uint16_t)bf16_bits(x);
-  const float r = x - __builtin_bit_cast(float, (uint32_t)hi << 16);
-  lo = (uint16_t)bf16_bits(r);
+__device__ __forceinline__ void split_bf16(float x, uint32_t& hi, uint32_t& lo) {
+  hi = bf16_bits(x);
+  lo = bf16_bits(x - __builtin_bit_cast(float, hi << 16));
 }
 
+// four consecutive elements per thread (K % 4 == 0)
 __global__ void __launch_bounds__(256) split_rows(const float* __restrict__ A, uint16_t* __restrict__ Ap, int M, int K) {
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (e >= (int64_t)M * K) return;
-  const int64_t m = e / K, k = e - m * K;
-  uint16_t hi, lo;
-  split_bf16(A[e], hi, lo);
+  const int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t per_row = K / 4;
+  if (v >= (int64_t)M * per_row) return;
+  const int64_t m = v / per_row, k = (v - m * per_row) * 4;
+  const f32x4 x = *reinterpret_cast<const f32x4*>(A + m * K + k);
+  uint32_t hi[4], lo[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) split_bf16(x[q], hi[q], lo[q]);
+  const u32x2 h = {hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
+  const u32x2 l = {lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
   uint16_t* row = Ap + m * 3 * K;
-  row[k] = hi;
-  row[K + k] = hi;
-  row[2 * K + k] = lo;
+  *reinterpret_cast<u32x2*>(row + k) = h;
+  *reinterpret_cast<u32x2*>(row + K + k) = h;
+  *reinterpret_cast<u32x2*>(row + 2 * K + k) = l;
 }
 
 __global__ void __launch_bounds__(256) split_transpose(const float* __restrict__ B, uint16_t* __restrict__ Bp, int K,
                                                        int N) {
-  __shared__ float tile[64][65];
-  const int k0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  constexpr int T = 64, ROW = T + 4;  // floats
+  __shared__ __attribute__((aligned(16))) float tile[T * ROW];
+  const int k0 = blockIdx.y * T, n0 = blockIdx.x * T;
   const int t = threadIdx.x;
-  for (int idx = t; idx < 64 * 64; idx += 256) {
-    const int r = idx >> 6, c = idx & 63;
-    const int k = k0 + r, n = n0 + c;
-    tile[r][c] = (k < K && n < N) ? B[(int64_t)k * N + n] : 0.f;
+  for (int idx = t; idx < T * (T / 4); idx += 256) {
+    const int r = idx / (T / 4), c = idx % (T / 4);
+    const int k = k0 + r, n = n0 + c * 4;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (k < K && n < N) v = *reinterpret_cast<const f32x4*>(B + (int64_t)k * N + n);  // N % 8 == 0
+    *reinterpret_cast<f32x4*>(tile + r * ROW + c * 4) = v;
   }
   __syncthreads();
-  for (int idx = t; idx < 64 * 64; idx += 256) {
-    const int r = idx >> 6, c = idx & 63;  // r: n, c: k
-    const int n = n0 + r, k = k0 + c;
-    if (k < K && n < N) {
-      uint16_t hi, lo;
-      split_bf16(tile[c][r], hi, lo);
-      uint16_t* row = Bp + (int64_t)n * 3 * K;
-      row[k] = hi;
-      row[K + k] = lo;
-      row[2 * K + k] = hi;
-    }
+  // output chunk: row n, 8 consecutive k, written to the three segments
+  for (int idx = t; idx < T * (T / 8); idx += 256) {
+    const int r = idx / (T / 8), c = idx % (T / 8);
+    const int n = n0 + r, k = k0 + c * 8;
+    if (n >= N || k >= K) continue;
+    uint32_t hi[8], lo[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) split_bf16(tile[(c * 8 + q) * ROW + r], hi[q], lo[q]);
+    const u32x4 h = {hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16)};
+    const u32x4 l = {lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16)};
+    uint16_t* row = Bp + (int64_t)n * 3 * K;
+    *reinterpret_cast<u32x4*>(row + k) = h;
+    *reinterpret_cast<u32x4*>(row + K + k) = l;
+    *reinterpret_cast<u32x4*>(row + 2 * K + k) = h;
   }
 }
 
@@ -479,6 +532,7 @@ extern "C" tb_status tb_matmul(int dtype, const void* a, const void* b, void* ou
   TB_CHECK_ARG(workspace && workspace_bytes >= need, "tb_matmul: needs a %lld-byte workspace (got %lld)",
                (long long)need, (long long)workspace_bytes);
   TB_CHECK_ALIGN(a, 16, "a");
+  TB_CHECK_ALIGN(b, 16, "b");
   TB_CHECK_ALIGN(workspace, 256, "workspace");
   TB_CHECK_ALIGN(out, 16, "out");
   const dim3 tgrid((unsigned)((N + 63) / 64), (unsigned)((K + 63) / 64));
@@ -487,7 +541,7 @@ extern "C" tb_status tb_matmul(int dtype, const void* a, const void* b, void* ou
   if (dtype == 0) {
     uint16_t* Ap = reinterpret_cast<uint16_t*>(ws);
     uint16_t* Bp = Ap + 3 * M * K;
-    hipLaunchKernelGGL(split_rows, dim3((unsigned)((M * K + 255) / 256)), dim3(256), 0, stream,
+    hipLaunchKernelGGL(split_rows, dim3((unsigned)((M * (K / 4) + 255) / 256)), dim3(256), 0, stream,
                        reinterpret_cast<const float*>(a), Ap, (int)M, (int)K);
     hipLaunchKernelGGL(split_transpose, tgrid, dim3(256), 0, stream, reinterpret_cast<const float*>(b), Bp, (int)K,
                        (int)N);
@@ -526,6 +580,7 @@ extern "C" tb_status tb_matmul_int8(const int8_t* a, const uint8_t* b, int32_t* 
   TB_CHECK_ARG(workspace && workspace_bytes >= need, "tb_matmul_int8: needs a %lld-byte workspace (got %lld)",
                (long long)need, (long long)workspace_bytes);
   TB_CHECK_ALIGN(a, 16, "a");
+  TB_CHECK_ALIGN(b, 16, "b");
   TB_CHECK_ALIGN(workspace, 256, "workspace");
   TB_CHECK_ALIGN(out, 16, "out");
   int8_t* bt = reinterpret_cast<int8_t*>(workspace);
