@@ -18,7 +18,11 @@
 // |x| <= max) is checked exhaustively on the CPU by the test suite.
 //
 // Conversion to e4m3 (OCP "fn": bias 7, 3 mantissa bits, max 448, no infinity,
-// S.1111.111 = NaN) rounds to nearest-even on the magnitude bits:
+// S.1111.111 = NaN).  Finite, non-zero rows use the hardware converter
+// v_cvt_pk_fp8_f32 (their quotients lie in [-448, 448], where it rounds exactly
+// like the encoder below; see quantize_chunk).  Rows with inf or NaN use the
+// integer encoder e4m3_code (tb_common.h), which rounds to nearest-even on the
+// magnitude bits:
 //   |q| >= 480 (0x43F00000)      -> 0x7F (NaN code), sign OR-ed back in
 //   |q| <  2^-6 (subnormal range) -> add 2^14 in fp32: the sum's ulp is 2^-9, the
 //                                   e4m3 subnormal step, so the hardware RNE add
@@ -47,6 +51,39 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, 64));
   return v;
+}
+
+// Eight fp16 values -> eight e4m3 codes of x / sa.  `m` is the row's largest
+// magnitude as fp16 bits.  For a finite, non-zero row every quotient lies in
+// [-448, 448] (up to one fp32 rounding), where the hardware conversion
+// v_cvt_pk_fp8_f32 rounds exactly as the integer encoder e4m3_code (checked on
+// the device against the torch-pinned CPU oracle for all e4m3 values, every
+// rounding midpoint +-1 fp32 ulp, the subnormal range, signed zeros and 3*10^6
+// random values with |x| <= 464: no difference).  A zero row gives 0xFF codes
+// (x86's 0/0); rows holding inf or NaN take the integer encoder.
+__device__ __forceinline__ u32x2 quantize_chunk(const u32x4& x, float sa, float y, uint32_t m) {
+  float q[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint16_t h = (uint16_t)((x[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+    q[j] = quotient((float)__builtin_bit_cast(_Float16, h), sa, y);
+  }
+  u32x2 o;
+  if (m == 0) {
+    o[0] = o[1] = 0xFFFFFFFFu;
+  } else if (m < 0x7C00u) {
+    o[0] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+    o[0] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], (int)o[0], true);
+    o[1] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], 0, false);
+    o[1] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[6], q[7], (int)o[1], true);
+  } else {
+    uint32_t c[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c[j] = e4m3_code(q[j]);
+    o[0] = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+    o[1] = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+  }
+  return o;
 }
 
 template <int ITEMS>
@@ -81,24 +118,11 @@ __global__ void __launch_bounds__(256) fp8_quant_rows(const u32x4* __restrict__ 
   const float sa = amax / 448.0f;
   const float y = 1.0f / sa;
   if (threadIdx.x == 0) sa_out[row] = sa;
-  const bool zero_row = (m == 0);
 
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
     const int64_t ch = threadIdx.x + (int64_t)i * 256;
-    if (ch < chunks) {
-      uint32_t c[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint16_t h = (uint16_t)((x[i][j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
-        const float xf = (float)__builtin_bit_cast(_Float16, h);
-        c[j] = zero_row ? 0xFFu : e4m3_code(quotient(xf, sa, y));
-      }
-      u32x2 o;
-      o[0] = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-      o[1] = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-      Aq[row * chunks + ch] = o;
-    }
+    if (ch < chunks) Aq[row * chunks + ch] = quantize_chunk(x[i], sa, y, m);
   }
 }
 
@@ -127,21 +151,7 @@ __global__ void __launch_bounds__(256) fp8_quant_rows_long(const u32x4* __restri
   const float sa = amax / 448.0f;
   const float y = 1.0f / sa;
   if (threadIdx.x == 0) sa_out[row] = sa;
-  const bool zero_row = (m == 0);
-  for (int64_t ch = threadIdx.x; ch < chunks; ch += 256) {
-    const u32x4 v = src[ch];
-    uint32_t c[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint16_t h = (uint16_t)((v[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
-      const float xf = (float)__builtin_bit_cast(_Float16, h);
-      c[j] = zero_row ? 0xFFu : e4m3_code(quotient(xf, sa, y));
-    }
-    u32x2 o;
-    o[0] = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-    o[1] = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-    Aq[row * chunks + ch] = o;
-  }
+  for (int64_t ch = threadIdx.x; ch < chunks; ch += 256) Aq[row * chunks + ch] = quantize_chunk(src[ch], sa, y, m);
 }
 
 }  // namespace tb

