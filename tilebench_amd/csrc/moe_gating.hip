@@ -1,15 +1,18 @@
 // MoE router gating: per row, top-k logits (descending, equal logits -> lowest
 // expert index first) and the softmax over those k logits in fp32.
 //
-// Layout: a block stages ROWS consecutive rows of logits in LDS with one
-// coalesced 16-byte sweep (the rows are contiguous in HBM), converting each
-// logit to an order-preserving uint32 key on the way in.  Each row is then
-// owned by LPR lanes (a power of two, consecutive lanes), each holding V keys
-// of that row in registers.  k selection rounds follow: every lane takes its
+// Layout: a row is owned by LPR consecutive lanes (a power of two), lane q
+// holding elements q*V .. q*V+V-1 (V = 16) in registers, loaded with 16-byte
+// loads: the lanes of a row read it with one contiguous sweep and consecutive
+// rows follow, so the logits stream straight from HBM into registers, with no
+// LDS staging and no barrier.  Each logit becomes an order-preserving
+// uint32 key.  k selection rounds follow: every lane takes its
 // largest remaining key (ascending index order, strict '>', so the lowest index
 // wins a tie), the LPR lanes combine (key, index) pairs with xor-shuffles, and
 // the owner of the winner clears it.  Selection runs on the logits themselves,
-// never on exp() values, so rounding in exp cannot create or break ties.
+// never on exp() values, so rounding in exp cannot create or break ties.  The
+// butterfly leaves every lane of the row with the same k winners, and lane t
+// writes output t (weights and indices of a row land in one coalesced store).
 //
 // Key map: k(x) = bits ^ 0x80000000 for x >= 0 and ~bits for x < 0, with -0.0
 // folded onto +0.0 (they compare equal) and every NaN mapped to 0xFFFFFFFF (a
@@ -62,71 +65,61 @@ __device__ __forceinline__ void store_weight(void* base, int64_t i, float w) {
 }
 
 constexpr int kBlock = 256;
-constexpr int kPad = 4;  // LDS row padding (dwords) against bank conflicts
-constexpr int kBatch = 8;  // 16-byte loads in flight per thread while staging
+
+// Exchange with the partner lane of butterfly step `step` inside a group of
+// LPR lanes.  Steps 0-3 (partners within 16 lanes) are DPP moves: quad swaps
+// (distance 1 and 2), then the half-row and row mirrors, which pair the two
+// 4-lane and the two 8-lane halves; any pairing that joins disjoint halves
+// gives the same maximum, and the (key, index) order is total.  Wider steps go
+// through the LDS crossbar (__shfl_xor).
+template <int LPR>
+__device__ __forceinline__ uint32_t xchg(uint32_t v, int step) {
+  switch (step) {
+    case 0: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+    case 1: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+    case 2: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    case 3: return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false);  // row_mirror
+    default: return (uint32_t)__shfl_xor((int)v, 1 << step, LPR);
+  }
+}
 
 template <int DT, int V, int LPR, int KMAX>
 __global__ void __launch_bounds__(kBlock) gating_kernel(const void* __restrict__ logits, void* __restrict__ weights,
                                                         int32_t* __restrict__ indices, int64_t M, int E, int k) {
   constexpr int ROWS = kBlock / LPR;
-  extern __shared__ uint32_t lds[];
-  const int stride = E + kPad;
-  const int64_t row0 = (int64_t)blockIdx.x * ROWS;
-  const int nrows = (int)((M - row0) < ROWS ? (M - row0) : ROWS);
+  constexpr int ESZ = DT == 0 ? 4 : 2;
+  const int64_t r = (int64_t)blockIdx.x * ROWS + threadIdx.x / LPR;
+  const int q = threadIdx.x % LPR;
+  if (r >= M) return;  // whole LPR groups leave together
 
-  // Stage the block's rows (contiguous in HBM) as keys.  Loads are issued in
-  // batches of kBatch independent 16-byte loads per thread before any of them
-  // is consumed, so one HBM round trip covers a batch.
+  // Keys of this lane's elements: one 16-byte load when the chunk lies inside
+  // the row and rows are 16-byte multiples (so the load is aligned), else
+  // element loads (never past the end of the row).
+  uint32_t u[V];
   {
-    const int64_t base = row0 * E;
-    const int total = nrows * E;
-    constexpr int EPV = DT == 0 ? 4 : 8;  // elements per 16-byte vector
-    if ((E % EPV) == 0) {
-      const u32x4* src = reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(logits) +
-                                                        base * (DT == 0 ? 4 : 2));
-      const int nvec = total / EPV;
-      for (int v0 = threadIdx.x; v0 < nvec; v0 += kBlock * kBatch) {
-        u32x4 x[kBatch];
+    const int c0 = q * V;
+    const char* rowp = reinterpret_cast<const char*>(logits) + (r * E + c0) * ESZ;
+    const bool aligned16 = ((E * ESZ) & 15) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0;
+    if (c0 + V <= E && aligned16) {
+      constexpr int NV = V * ESZ / 16;
+      u32x4 x[NV];
 #pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-          const int v = v0 + b * kBlock;
-          if (v < nvec) x[b] = src[v];
+      for (int b = 0; b < NV; ++b) x[b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rowp) + b);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        uint32_t fb;
+        if constexpr (DT == 0) {
+          fb = x[j / 4][j % 4];
+        } else {
+          const uint32_t h = (x[j / 8][(j % 8) >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+          fb = DT == 1 ? __builtin_bit_cast(uint32_t, (float)__builtin_bit_cast(_Float16, (uint16_t)h)) : (h << 16);
         }
-#pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-          const int v = v0 + b * kBlock;
-          if (v < nvec) {
-            const int e = v * EPV, r = e / E, c = e - r * E;
-#pragma unroll
-            for (int t = 0; t < EPV; ++t) {
-              uint32_t fb;
-              if constexpr (DT == 0) {
-                fb = x[b][t];
-              } else {
-                const uint32_t h = (x[b][t >> 1] >> (16 * (t & 1))) & 0xFFFFu;
-                fb = DT == 1 ? __builtin_bit_cast(uint32_t, (float)__builtin_bit_cast(_Float16, (uint16_t)h))
-                             : (h << 16);
-              }
-              lds[r * stride + c + t] = key_of_bits(fb);
-            }
-          }
-        }
+        u[j] = key_of_bits(fb);
       }
     } else {
-      for (int e = threadIdx.x; e < total; e += kBlock) lds[(e / E) * stride + e % E] = load_key<DT>(logits, base + e);
-    }
-  }
-  __syncthreads();
-
-  const int r = threadIdx.x / LPR;
-  const int q = threadIdx.x % LPR;
-  if (r >= nrows) return;  // whole LPR groups leave together (nrows is uniform)
-
-  uint32_t u[V];
 #pragma unroll
-  for (int j = 0; j < V; ++j) {
-    const int c = q * V + j;
-    u[j] = c < E ? lds[r * stride + c] : 0u;
+      for (int j = 0; j < V; ++j) u[j] = c0 + j < E ? load_key<DT>(logits, r * E + c0 + j) : 0u;
+    }
   }
 
   uint32_t sel_u[KMAX];
@@ -143,9 +136,9 @@ __global__ void __launch_bounds__(kBlock) gating_kernel(const void* __restrict__
         bi = gt ? q * V + j : bi;
       }
 #pragma unroll
-      for (int off = 1; off < LPR; off <<= 1) {
-        const uint32_t ou = __shfl_xor(bu, off, LPR);
-        const int oi = __shfl_xor(bi, off, LPR);
+      for (int step = 0; (1 << step) < LPR; ++step) {
+        const uint32_t ou = xchg<LPR>(bu, step);
+        const int oi = (int)xchg<LPR>((uint32_t)bi, step);
         const bool take = ou > bu || (ou == bu && oi < bi);
         bu = take ? ou : bu;
         bi = take ? oi : bi;
@@ -157,7 +150,7 @@ __global__ void __launch_bounds__(kBlock) gating_kernel(const void* __restrict__
     }
   }
 
-  if (q != 0) return;
+  // softmax over the k selected logits in fp32, summed in selection order
   const float v0 = float_of_key(sel_u[0]);
   float e[KMAX];
   float sum = 0.f;
@@ -168,10 +161,10 @@ __global__ void __launch_bounds__(kBlock) gating_kernel(const void* __restrict__
       sum += e[t];
     }
   }
-  const int64_t out0 = (row0 + r) * k;
+  const int64_t out0 = r * k;
 #pragma unroll
   for (int t = 0; t < KMAX; ++t) {
-    if (t < k) {
+    if (t < k && t % LPR == q) {
       store_weight<DT>(weights, out0 + t, e[t] / sum);
       indices[out0 + t] = sel_i[t];
     }
@@ -182,9 +175,8 @@ template <int DT, int V, int LPR, int KMAX>
 static tb_status launch(const void* logits, void* weights, int32_t* indices, int64_t M, int E, int k,
                         hipStream_t stream) {
   constexpr int ROWS = kBlock / LPR;
-  const size_t lds = (size_t)ROWS * (E + kPad) * sizeof(uint32_t);
   const int64_t blocks = (M + ROWS - 1) / ROWS;
-  hipLaunchKernelGGL((gating_kernel<DT, V, LPR, KMAX>), dim3((unsigned)blocks), dim3(kBlock), lds, stream, logits,
+  hipLaunchKernelGGL((gating_kernel<DT, V, LPR, KMAX>), dim3((unsigned)blocks), dim3(kBlock), 0, stream, logits,
                      weights, indices, M, E, k);
   return launch_status("tb_moe_topk_gating");
 }
@@ -192,15 +184,16 @@ static tb_status launch(const void* logits, void* weights, int32_t* indices, int
 template <int DT, int KMAX>
 static tb_status dispatch_shape(const void* logits, void* weights, int32_t* indices, int64_t M, int E, int k,
                                 hipStream_t stream) {
-  // Lanes per row: enough that V <= 16 values per lane for E <= 64 (fills all
-  // four SIMDs of every CU at M = 16k rows) and V = 64 beyond.
+  // 16 elements per lane (four 16-byte loads in fp32, two in fp16/bf16) and
+  // as many lanes per row as that takes: measured on E in {64, 128, 256}, 16
+  // per lane beats 8 (more butterfly work per row) and 32 (fewer wavefronts).
   if (E <= 16) return launch<DT, 16, 1, KMAX>(logits, weights, indices, M, E, k, stream);
   if (E <= 32) return launch<DT, 16, 2, KMAX>(logits, weights, indices, M, E, k, stream);
   if (E <= 64) return launch<DT, 16, 4, KMAX>(logits, weights, indices, M, E, k, stream);
-  if (E <= 128) return launch<DT, 32, 4, KMAX>(logits, weights, indices, M, E, k, stream);
-  if (E <= 256) return launch<DT, 64, 4, KMAX>(logits, weights, indices, M, E, k, stream);
-  if (E <= 512) return launch<DT, 64, 8, KMAX>(logits, weights, indices, M, E, k, stream);
-  return launch<DT, 64, 16, KMAX>(logits, weights, indices, M, E, k, stream);
+  if (E <= 128) return launch<DT, 16, 8, KMAX>(logits, weights, indices, M, E, k, stream);
+  if (E <= 256) return launch<DT, 16, 16, KMAX>(logits, weights, indices, M, E, k, stream);
+  if (E <= 512) return launch<DT, 16, 32, KMAX>(logits, weights, indices, M, E, k, stream);
+  return launch<DT, 16, 64, KMAX>(logits, weights, indices, M, E, k, stream);
 }
 
 template <int DT>
