@@ -1,0 +1,214 @@
+"""Capture validation and kernel classification for the hip backend's
+profiling, the CPU tests of tests/test_rocprof_compute.py:75-171 restated for
+rocprofv3's kernel-trace and counter-collection CSVs."""
+import csv
+import re
+
+import pytest
+
+from tilebench_amd.profiling import capture as cp
+from tilebench_amd.profiling import kernels as kn
+
+#: one run of a two-kernel operator that launches its GEMM twice
+PIPELINE = ["tb::ntg::unpack_i2_tile", "tb::ntg::nt_gemm<3, 4, 128, 128, 64, 64>",
+            "tb::ntg::unpack_i2_tile", "tb::ntg::nt_gemm<3, 4, 128, 128, 64, 64>"]
+
+TRACE_HEADER = ["Kind", "Agent_Id", "Queue_Id", "Stream_Id", "Thread_Id", "Dispatch_Id", "Kernel_Id",
+                "Kernel_Name", "Correlation_Id", "Start_Timestamp", "End_Timestamp"]
+COUNTER_HEADER = ["Correlation_Id", "Dispatch_Id", "Agent_Id", "Queue_Id", "Process_Id", "Thread_Id",
+                  "Grid_Size", "Kernel_Id", "Kernel_Name", "Workgroup_Size", "Counter_Name", "Counter_Value",
+                  "Start_Timestamp", "End_Timestamp"]
+
+
+def _trace(path, launches, start=1000):
+    """A kernel-trace CSV, rows deliberately written out of launch order."""
+    rows = [["KERNEL_DISPATCH", "Agent 1", 1, 0, 7, i + 1, 9, n, i + 1, start + 10 * i, start + 10 * i + 5]
+            for i, n in enumerate(launches)]
+    with open(path, "w", newline="") as fh:
+        w = csv.writer(fh)
+        w.writerow(TRACE_HEADER)
+        w.writerows(rows[::-1])
+    return path
+
+
+def _counters(path, launches, counters=("FETCH_SIZE", "WRITE_SIZE")):
+    """A counter-collection CSV: one row per (dispatch, counter)."""
+    with open(path, "w", newline="") as fh:
+        w = csv.writer(fh)
+        w.writerow(COUNTER_HEADER)
+        for i, n in enumerate(launches):
+            for c in counters:
+                w.writerow([i + 1, i + 1, "Agent 1", 1, 1, 1, 4096, 3, n, 256, c, 1.0, 500 + i, 600 + i])
+    return path
+
+
+@pytest.mark.parametrize("name", [
+    "at::native::vectorized_elementwise_kernel<4, at::native::FillFunctor<float>>",
+    "void at::native::elementwise_kernel<128, 2>(int, void)",
+    "__amd_rocclr_copyBuffer", "__amd_rocclr_fillBufferAligned", "Memcpy DtoD", "hipMemsetAsync", "",
+    "Cijk_Ailk_Bljk_HHS_BH_MT128x128x32", "tbx::fake_kernel", "my_tb::kernel"])
+def test_runtime_library_and_aten_kernels_are_not_operator_kernels(name):
+    assert kn.is_aux_kernel(name)
+    assert not kn.is_backend_kernel(name)
+
+
+@pytest.mark.parametrize("name", [
+    "tb::w4a16::w4a16_prefill", "void tb::w4a16::w4a16_decode(__half const*, unsigned char const*)",
+    "tb::ntg::nt_gemm<1, 2, 256, 256, 128, 64>", "tb::gating_kernel<0, 16, 4, 8>", "tb::copy_kernel"])
+def test_backend_kernels_are_operator_kernels(name):
+    assert kn.is_backend_kernel(name)
+    assert not kn.is_aux_kernel(name)
+
+
+def test_stem_drops_return_type_and_argument_list_but_keeps_template_arguments():
+    assert kn.kernel_stem("void tb::ntg::nt_gemm<1, 2, 256, 256, 128, 64>(unsigned char const*, int)") == \
+        "tb::ntg::nt_gemm<1, 2, 256, 256, 128, 64>"
+    assert kn.kernel_stem("tb::fp8_quant_rows<4>") == "tb::fp8_quant_rows<4>"
+    assert kn.kernel_stem("void tb::f<(tb::Kind)1>(float*)") == "tb::f<(tb::Kind)1>"
+
+
+def test_kernel_filter_is_start_anchored_never_end_anchored_and_escaped():
+    rgx = kn.kernel_filter_regex(PIPELINE + ["at::native::fill"])
+    assert rgx.startswith("^") and "$" not in rgx
+    pat = re.compile(rgx)
+    for n in PIPELINE:
+        assert pat.match(n) and pat.match("void " + n + "(int*, int)")
+    assert not pat.match("tb::ntg::nt_gemm<3, 4, 256, 256, 128, 64>")   # other template arguments
+    assert not pat.match("xtb::ntg::unpack_i2_tile")                     # start-anchored
+    assert not pat.match("tb::ntgXunpack_i2_tile")                        # `:` and `<` are literal
+    with pytest.raises(ValueError):
+        kn.kernel_filter_regex(["at::native::fill"])
+
+
+def test_repeated_launches_are_counted_not_deduplicated(tmp_path):
+    f = _trace(tmp_path / "run_kernel_trace.csv", PIPELINE)
+    assert cp.dispatch_sequence(f) == PIPELINE
+    g = _counters(tmp_path / "run_counter_collection.csv", PIPELINE)
+    assert cp.dispatch_sequence(g) == PIPELINE          # two rows per dispatch, counted once
+    v = cp.validate_capture([f, g], PIPELINE)
+    assert v["ok"] and v["captured_names"] == PIPELINE
+    assert set(v["launches_per_file"].values()) == {4}
+
+
+def test_argument_lists_in_the_capture_do_not_matter(tmp_path):
+    f = _trace(tmp_path / "t.csv", ["void " + n + "(int)" for n in PIPELINE])
+    assert cp.validate_capture(f, PIPELINE)["ok"]
+
+
+def test_a_missing_launch_fails_even_when_every_name_is_right(tmp_path):
+    f = _trace(tmp_path / "t.csv", PIPELINE)
+    g = _counters(tmp_path / "c.csv", PIPELINE[:3])
+    v = cp.validate_capture([f, g], PIPELINE)
+    assert not v["ok"]
+    assert any("c.csv" in p and "captured 3 != expected 4" in p for p in v["problems"])
+
+
+@pytest.mark.parametrize("intruder", ["__amd_rocclr_copyBuffer", "at::native::vectorized_elementwise_kernel<4>"])
+def test_a_non_operator_kernel_in_the_capture_fails(tmp_path, intruder):
+    f = _trace(tmp_path / "t.csv", PIPELINE[:2] + [intruder] + PIPELINE[2:])
+    v = cp.validate_capture(f, PIPELINE)
+    assert not v["ok"] and any("non-operator" in p for p in v["problems"])
+
+
+def test_launch_order_is_checked(tmp_path):
+    f = _trace(tmp_path / "t.csv", [PIPELINE[1], PIPELINE[0]] + PIPELINE[2:])
+    v = cp.validate_capture(f, PIPELINE)
+    assert not v["ok"] and any("order differs at launch 0" in p for p in v["problems"])
+
+
+def test_an_unexpected_backend_kernel_fails(tmp_path):
+    other = ["tb::ntg::unpack_i2_tile", "tb::ntg::nt_gemm<3, 4, 256, 256, 128, 64>"] * 2
+    v = cp.validate_capture(_trace(tmp_path / "t.csv", other), PIPELINE)
+    assert not v["ok"] and any("unexpected kernels" in p for p in v["problems"])
+
+
+def test_an_empty_or_absent_capture_fails(tmp_path):
+    assert cp.sequence_problems(PIPELINE, []) == ["nothing captured"]
+    v = cp.validate_capture(_trace(tmp_path / "t.csv", []), PIPELINE)
+    assert not v["ok"] and any("nothing captured" in p for p in v["problems"])
+    v = cp.validate_capture(tmp_path / "absent.csv", PIPELINE)
+    assert not v["ok"] and any("missing" in p for p in v["problems"])
+    assert not cp.validate_capture([], PIPELINE)["ok"]
+
+
+def test_probe_needs_a_gpu(monkeypatch, capsys):
+    import torch
+    from tilebench_amd.profiling import probe
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    assert probe.main(["--ops", "w4a16_gemm"]) == 2
+    assert "needs a GPU" in capsys.readouterr().err
+
+
+@pytest.mark.parametrize("mangled,stem", [
+    ("_ZN2tb5w4a1613w4a16_prefillEPKDF16_PKhS2_S4_PDF16_iiiiii", "tb::w4a16::w4a16_prefill"),
+    ("_ZN2tb13gating_kernelILi0ELi16ELi16ELi2EEEvPKvPvPilii", "tb::gating_kernel<0, 16, 16, 2>"),
+    ("_ZN2tb11copy_kernelEPKDv4_jPS0_l", "tb::copy_kernel"),
+])
+def test_mangled_symbols_as_the_profilers_report_them(mangled, stem):
+    """torch.profiler names a HIP kernel by its mangled symbol, rocprofv3 by
+    the demangled name (or the mangled one when its demangler cannot read
+    `DF16_`).  Every spelling classifies and compares alike, and the filter
+    regex selects the mangled one too."""
+    assert kn.is_backend_kernel(mangled) and not kn.is_aux_kernel(mangled)
+    assert kn.kernel_stem(mangled) == stem
+    assert cp.sequence_problems([mangled], [stem]) == []
+    assert re.match(kn.kernel_filter_regex([stem]), mangled)
+    assert kn.demangle("_Znot_a_symbol") == "_Znot_a_symbol"
+    assert kn.is_aux_kernel("_ZN2at6native29vectorized_elementwise_kernelILi4ENS0_11FillFunctorIfEEEEviT0_T1_")
+
+
+def test_every_kernel_of_the_built_library_is_a_backend_kernel():
+    """Each tb:: symbol of libtbhip.so (kernel launch stubs carry the kernel's
+    mangled name) demangles into the tb:: namespace, so the probe never drops
+    one of the backend's launches whatever its argument types."""
+    import shutil
+    import subprocess
+    from pathlib import Path
+    lib = Path(__file__).resolve().parent.parent / "tilebench_amd" / "libtbhip.so"
+    if not lib.is_file() or shutil.which("nm") is None:
+        pytest.skip("libtbhip.so not built")
+    out = subprocess.run(["nm", str(lib)], capture_output=True, text=True, check=True).stdout
+    syms = sorted({ln.split()[-1] for ln in out.splitlines()
+                   if len(ln.split()) == 3 and ln.split()[1] in "Tt" and ln.split()[-1].startswith("_ZN2tb")})
+    assert len(syms) > 20
+    for s in syms:
+        text = kn.demangle(s)
+        assert text != s, s                       # every spelling demangles
+        if text.startswith(("tb::", "void tb::")):  # kernels return void; templated helpers name their type
+            assert kn.is_backend_kernel(s) and kn.kernel_stem(s).startswith("tb::"), text
+
+
+def test_filter_regex_under_the_cxx_regex_grammar(tmp_path):
+    """rocprofv3 compiles its kernel filter with std::regex (ECMAScript):
+    check the filter in that grammar itself, on the names rocprofv3 prints."""
+    import shutil
+    import subprocess
+    if shutil.which("g++") is None:
+        pytest.skip("no g++")
+    src = tmp_path / "rx.cpp"
+    src.write_text('#include <regex>\n#include <iostream>\n#include <string>\n'
+                   'int main(int c, char** v) {\n'
+                   '  std::regex r(v[1], v[2][0] == \'e\' ? std::regex::extended : std::regex::ECMAScript);\n'
+                   '  std::string s;\n'
+                   '  while (std::getline(std::cin, s)) std::cout << std::regex_search(s, r) << "\\n"; }\n')
+    exe = tmp_path / "rx"
+    subprocess.run(["g++", "-O0", "-o", str(exe), str(src)], check=True)
+    rgx = kn.kernel_filter_regex(PIPELINE + ["tb::w4a16::w4a16_decode"])
+    assert "\\ " not in rgx and "(?" not in rgx
+    # the signatures rocprofv3 matches in counter collection: `void ` before templates only
+    names = ["tb::ntg::unpack_i2_tile(unsigned char const*, signed char*, int, int)",
+             "void tb::ntg::nt_gemm<3, 4, 128, 128, 64, 64>(unsigned char const*, unsigned char const*, void*, int)",
+             "tb::w4a16::w4a16_decode(_Float16 const*, int)",
+             "void tb::ntg::nt_gemm<3, 4, 256, 256, 128, 64>(unsigned char const*, unsigned char const*, void*, int)",
+             "tb::w4a16::w4a16_prefill(_Float16 const*, int)",
+             "void at::native::vectorized_elementwise_kernel<4>(int)", "__amd_rocclr_copyBuffer",
+             "xtb::ntg::unpack_i2_tile(int)",
+             # left mangled by rocprofv3 when it cannot demangle `DF16_`
+             "_ZN2tb5w4a1612w4a16_decodeEPKDF16_PKhS2_S4_PDF16_PfPiiiiii",
+             "_ZN2tb3ntg7nt_gemmILi3ELi4ELi128ELi128ELi64ELi64EEEvPKhS3_Pviii",
+             "_ZN2tb3ntg7nt_gemmILi3ELi4ELi256ELi256ELi128ELi64EEEvPKhS3_Pviii",
+             "_ZN2tb5w4a1613w4a16_prefillEPKDF16_PKhS2_S4_PDF16_iiiiii"]
+    for grammar in ("ecma", "extended"):
+        out = subprocess.run([str(exe), rgx, grammar], input="\n".join(names) + "\n", capture_output=True,
+                             text=True, check=True).stdout.split()
+        assert out == ["1", "1", "1", "0", "0", "0", "0", "0", "1", "1", "0", "0"], grammar
