@@ -219,6 +219,34 @@ def _w_grouped():
                 inputs=inputs, step=lambda x: impl_hip.run(*x), kernel="tb::w4a16::w4a16_grouped", cpu_sample=cpu_sample)
 
 
+def _w_fused_moe():
+    from tilebench_amd.data import tensors as T
+    from tilebench_amd.benchmarks.operators.fused_moe_w4a16 import impl_hip
+
+    tokens, E, topk, H, I, G13, G2 = 16384, 64, 8, 4096, 704, 128, 64
+    flops = 6 * tokens * topk * H * I           # gate/up 2*T*k*H*2I + down 2*T*k*I*H
+    wbytes = E * (H * I + (H // G13) * 2 * I * 2 + (H // G13) * I + I * H // 2 + (I // G2) * H * 2 + (I // G2) * H // 2)
+    nbytes = 2 * tokens * H + 4 * tokens * E + wbytes + 2 * tokens * H
+
+    def inputs():
+        return T.generate_fused_moe_w4a16_inputs(tokens, E, topk, H, I, G13, G2, seed=15, device="cuda")
+
+    def cpu_sample():
+        import oracle
+        x = T.generate_fused_moe_w4a16_inputs(256, E, topk, H, I, G13, G2, seed=15, device="cpu")
+        x = [t.numpy() if hasattr(t, "numpy") else t for t in x]
+        return ((lambda: oracle.fused_moe_w4a16(*x)), 6 * 256 * topk * H * I,
+                "256 of 16384 tokens through the whole layer, all 64 experts (numpy dequant + fp32 BLAS)")
+
+    return dict(name="fused_moe_w4a16",
+                config={"workload": "fused_moe_w4a16", "tokens": tokens, "experts": E, "topk": topk, "H": H, "I": I,
+                        "group13": G13, "group2": G2, "zipf_s": 1.1},
+                metric="MoE layer (gating + sort + W4A16 gate/up + SiLU + W4A16 down + combine) throughput",
+                unit="TFLOP/s", dtype="fp16 x int4 -> fp16 (fp32 acc)", bound="mfma", peak_key="fp16",
+                bytes=nbytes, flops=flops, out_bytes=2 * tokens * H, inputs=inputs, step=lambda x: impl_hip.run(*x),
+                kernel="tb::w4a16::moe_gate_up", cpu_sample=cpu_sample)
+
+
 def _w_weight_dequant():
     import torch
     from tilebench_amd.data import tensors as T
@@ -381,6 +409,7 @@ WORKLOADS = {
     "fp8_act_quant": _w_fp8_quant,
     "fp8_scaled_gemm": _w_fp8_gemm,
     "moe_w4a16_grouped_gemm": _w_grouped,
+    "fused_moe_w4a16": _w_fused_moe,
     "weight_dequant": _w_weight_dequant,
     "dequantize_rowwise": _w_dequantize_rowwise,
     "quantize_global": _w_quantize_global,

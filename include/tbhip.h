@@ -130,6 +130,63 @@ tb_status tb_moe_w4a16_grouped_gemm(const uint16_t* A, const uint8_t* W, const u
                                     int64_t experts, int64_t N, int64_t K, int64_t group, hipStream_t stream);
 
 /*
+ * MoE layer around the grouped W4A16 GEMM (the pipeline's steps are also
+ * exported one by one).  Pairs p = t * topk + j are (token, slot) pairs.
+ *
+ * tb_moe_align: topk_ids int32 [pairs] -> sorted_ids int32 [n_valid], the
+ *   pair ids ordered by expert and, within an expert, by p; offsets int32
+ *   [E + 1], offsets[e] = number of pairs with an id < e.  Ids outside [0, E)
+ *   are routed nowhere.  pairs < 2^31, E <= 4096.
+ *
+ * tb_moe_w4a16_gate_up: for sorted row m of expert e (offsets[e] <= m <
+ *   offsets[e+1]), token t = sorted_ids[m] / topk:
+ *     h = fp16(X[t] @ dequant(W13_e)), W13_e int4 [H, 2I] (gate columns 0..I-1,
+ *     up columns I..2I-1; packed uint8 [E, H, I], scales fp16 [E, H/G, 2I],
+ *     zeros uint8 [E, H/G, I]),
+ *     act[m, c] = fp16(silu(fp32(h[c])) * fp32(h[I + c])), silu(x) = x / (1 + exp(-x)).
+ *   Requires I % 8 == 0, H % 64 == 0, G % 64 == 0, H % G == 0.
+ *
+ * tb_moe_w4a16_down: Y[sorted_ids[m]] = fp16(w[sorted_ids[m]] * (act[m] @
+ *   dequant(W2_e))) with fp32 weights w [pairs], W2 int4 [E, I, H] (packed
+ *   uint8 [E, I, H/2], scales fp16 [E, I/G, H], zeros uint8 [E, I/G, H/2]).
+ *   Rows of pairs routed nowhere are not written.  Requires H % 8 == 0,
+ *   I % 64 == 0, G % 64 == 0, I % G == 0.
+ *
+ * tb_moe_combine: out[t] = fp16(sum over slots j in order, skipping ids
+ *   outside [0, E), of fp32(Y[t * topk + j])), out fp16 [tokens, H].
+ *
+ * tb_fused_moe_w4a16: the five steps on one stream: tb_moe_topk_gating of
+ *   fp32 router logits [tokens, E] (top-k, softmax over the k values), align,
+ *   gate_up, down, combine.  The caller's workspace (size from
+ *   tb_fused_moe_w4a16_workspace_size, 256-byte aligned, no clearing needed)
+ *   holds weights, ids, the sorted rows, act [pairs, I] and Y [pairs, H].
+ *   Requires E <= 1024, topk <= 32, H % 64 == 0, I % 64 == 0, group13 | H,
+ *   group2 | I, both groups multiples of 64.
+ * Replaces: no reference operator.  The steps follow the reference's
+ *   moe_topk_gating (moe_topk_gating/impl_torch.py:4-20) and the config-4
+ *   grouped GEMM; the layer itself is the MoE feed-forward block around them.
+ */
+tb_status tb_moe_align(const int32_t* topk_ids, int64_t pairs, int64_t experts, int32_t* sorted_ids,
+                       int32_t* offsets, hipStream_t stream);
+tb_status tb_moe_w4a16_gate_up(const uint16_t* X, const int32_t* sorted_ids, const int32_t* offsets,
+                               const uint8_t* W13, const uint16_t* S13, const uint8_t* Z13, uint16_t* act,
+                               int64_t tokens, int64_t topk, int64_t experts, int64_t H, int64_t I, int64_t group,
+                               hipStream_t stream);
+tb_status tb_moe_w4a16_down(const uint16_t* act, const int32_t* sorted_ids, const int32_t* offsets,
+                            const float* topk_weights, const uint8_t* W2, const uint16_t* S2, const uint8_t* Z2,
+                            uint16_t* Y, int64_t pairs, int64_t experts, int64_t I, int64_t H, int64_t group,
+                            hipStream_t stream);
+tb_status tb_moe_combine(const uint16_t* y, const int32_t* topk_ids, uint16_t* out, int64_t tokens, int64_t topk,
+                         int64_t experts, int64_t H, hipStream_t stream);
+tb_status tb_fused_moe_w4a16_workspace_size(int64_t tokens, int64_t topk, int64_t experts, int64_t H, int64_t I,
+                                            int64_t* bytes);
+tb_status tb_fused_moe_w4a16(const uint16_t* X, const float* logits, const uint8_t* W13, const uint16_t* S13,
+                             const uint8_t* Z13, const uint8_t* W2, const uint16_t* S2, const uint8_t* Z2,
+                             uint16_t* out, int64_t tokens, int64_t experts, int64_t topk, int64_t H, int64_t I,
+                             int64_t group13, int64_t group2, void* workspace, int64_t workspace_bytes,
+                             hipStream_t stream);
+
+/*
  * Row/column-scaled fp8 GEMM (step 2):
  *   Y bf16 [M, N] = bf16(sa[m] * sw[n] * sum_k e4m3(Aq[m,k]) * e4m3(Wq[k,n])),
  *   fp32 accumulation on the e4m3 matrix cores, one RNE rounding.

@@ -27,6 +27,13 @@ BASELINE config text):
 * matmul_int8       — matmul_int8/impl_torch.py:4-19 (2-bit unpack, value - 1, exact).
 * matmul_*          — matmul_fp32_fp16_fp8/impl_torch.py:21-27 (matmul; fp8 through
                       a unit-scale _scaled_mm to bf16 and a cast back to e4m3).
+* MoE layer         — no reference operator: moe_topk_gating (above), a stable
+                      sort of the (token, slot) pairs by expert (the order the
+                      config-4 input generator lays rows out in,
+                      tilebench_amd/data/tensors.py sorted_padded_layout),
+                      the config-4 grouped W4A16 product twice (gate/up with
+                      SiLU * up in fp32 between, down scaled by the routing
+                      weight) and an in-order fp32 sum over each token's slots.
 
 How each function is pinned (tests/test_oracle.py): closed forms and exact
 rational arithmetic (dequant), the torch CPU fp8 cast over every fp16 value and
@@ -55,4 +62,10 @@ from .core import (  # noqa: F401
     matmul_f16,
     matmul_f32,
     matmul_fp8,
+    moe_align,
+    silu_mul,
+    moe_gate_up,
+    moe_down,
+    moe_combine,
+    fused_moe_w4a16,
 )

@@ -212,6 +212,100 @@ def moe_topk_gating(logits: np.ndarray, k: int, dtype: str = "fp32"):
     return w, order.astype(np.int32)
 
 
+# ----------------------------------------------------------------------------- MoE layer
+
+
+def moe_align(topk_ids: np.ndarray, experts: int):
+    """(token, slot) pair ids p = t * topk + j (the flattened index of
+    topk_ids [T, k]) ordered by expert and, within an expert, by p; ids outside
+    [0, E) are routed nowhere.  Returns (sorted_ids int32 [n_valid], offsets
+    int32 [E + 1]), offsets[e] = number of pairs with an id below e."""
+    flat = np.asarray(topk_ids).reshape(-1).astype(np.int64)
+    valid = (flat >= 0) & (flat < experts)
+    pid = np.nonzero(valid)[0]
+    order = np.argsort(flat[pid], kind="stable")
+    counts = np.bincount(flat[pid], minlength=experts)
+    offsets = np.zeros(experts + 1, dtype=np.int64)
+    offsets[1:] = np.cumsum(counts)
+    return pid[order].astype(np.int32), offsets.astype(np.int32)
+
+
+def silu_mul(h: np.ndarray) -> np.ndarray:
+    """fp16 [R, I] = fp16(silu(g) * u) of fp16 h [R, 2I] = [g | u] (gate in the
+    first half), silu(x) = x / (1 + exp(-x)), every step in fp32."""
+    h = np.asarray(h, dtype=np.float16)
+    I = h.shape[-1] // 2
+    g = h[..., :I].astype(np.float32)
+    u = h[..., I:].astype(np.float32)
+    with np.errstate(over="ignore"):   # exp(-g) and the fp16 cast may overflow to inf, as on the device
+        den = (np.float32(1.0) + np.exp(-g)).astype(np.float32)
+        return ((g / den).astype(np.float32) * u).astype(np.float16)
+
+
+def moe_gate_up(X: np.ndarray, sorted_ids: np.ndarray, offsets: np.ndarray, topk: int, packed: np.ndarray,
+                scales: np.ndarray, zeros: np.ndarray, group: int) -> np.ndarray:
+    """Sorted row m of expert e reads token sorted_ids[m] // topk of X fp16
+    [T, H]; act [n_valid, I] = silu_mul(fp16(X[t] @ dequant(W13_e))) with
+    W13 int4 [E, H, 2I] (packed [E, H, I], scales [E, H/G, 2I], zeros
+    [E, H/G, I])."""
+    E = packed.shape[0]
+    I = packed.shape[2]
+    act = np.zeros((len(sorted_ids), I), dtype=np.float16)
+    tok = np.asarray(sorted_ids, dtype=np.int64) // topk
+    for e in range(E):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        if hi > lo:
+            act[lo:hi] = silu_mul(w4a16_gemm(X[tok[lo:hi]], packed[e], scales[e], zeros[e], group))
+    return act
+
+
+def moe_down(act: np.ndarray, sorted_ids: np.ndarray, offsets: np.ndarray, weights: np.ndarray, pairs: int,
+             packed: np.ndarray, scales: np.ndarray, zeros: np.ndarray, group: int):
+    """Y [pairs, H] fp16: row sorted_ids[m] = fp16(w[sorted_ids[m]] * fp32(act[m]
+    @ dequant(W2_e))) (the fp32 product rounded once, to fp16, after the
+    weight), W2 int4 [E, I, H].  Returns (Y, written), `written` marking the
+    rows a pair of a valid expert produced (the kernel leaves the others)."""
+    E = packed.shape[0]
+    H = packed.shape[2] * 2
+    Y = np.zeros((pairs, H), dtype=np.float16)
+    written = np.zeros(pairs, dtype=bool)
+    w = np.asarray(weights, dtype=np.float32).reshape(-1)
+    sid = np.asarray(sorted_ids, dtype=np.int64)
+    for e in range(E):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        if hi > lo:
+            Wd = int4_dequant(packed[e], scales[e], zeros[e], group).astype(np.float32)
+            acc = (act[lo:hi].astype(np.float32) @ Wd).astype(np.float32)
+            rows = sid[lo:hi]
+            Y[rows] = (acc * w[rows][:, None]).astype(np.float32).astype(np.float16)
+            written[rows] = True
+    return Y, written
+
+
+def moe_combine(Y: np.ndarray, topk_ids: np.ndarray, experts: int) -> np.ndarray:
+    """out fp16 [T, H] = fp16(sum over slots j in order of fp32(Y[t * k + j])),
+    slots routed nowhere skipped."""
+    ids = np.asarray(topk_ids)
+    T, k = ids.shape
+    valid = (ids >= 0) & (ids < experts)
+    Yr = Y.reshape(T, k, -1)
+    acc = np.zeros((T, Yr.shape[2]), dtype=np.float32)
+    for j in range(k):
+        acc = np.where(valid[:, j:j + 1], (acc + Yr[:, j].astype(np.float32)).astype(np.float32), acc)
+    return acc.astype(np.float16)
+
+
+def fused_moe_w4a16(X, logits, W13, S13, Z13, W2, S2, Z2, topk: int, group13: int, group2: int) -> np.ndarray:
+    """The MoE layer: gating of fp32 logits [T, E] (moe_topk_gating), align,
+    gate/up with SiLU * up, down scaled by the routing weight, combine."""
+    T, E = np.asarray(logits).shape
+    w, ids = moe_topk_gating(np.asarray(logits, dtype=np.float32), topk, "fp32")
+    sid, off = moe_align(ids, E)
+    act = moe_gate_up(np.asarray(X, dtype=np.float16), sid, off, topk, W13, S13, Z13, group13)
+    Y, _ = moe_down(act, sid, off, w, T * topk, W2, S2, Z2, group2)
+    return moe_combine(Y, ids, E)
+
+
 # ----------------------------------------------------------------------------- reference analog operators
 
 

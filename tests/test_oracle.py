@@ -445,3 +445,120 @@ def test_matmul_fp8_oracle_matches_torch_casts():
     # fp32 vs float64 accumulation may move a bf16 rounding by one ulp on rare values
     assert (got == ref).mean() > 0.99
     assert np.abs(oracle.e4m3_to_f32(got) - oracle.e4m3_to_f32(ref)).max() <= 2.0 ** -6
+
+
+# ----------------------------------------------------------------------------- MoE layer
+
+
+def test_moe_align_brute_force_with_unrouted_ids():
+    rng = np.random.default_rng(21)
+    E = 7
+    ids = rng.integers(-2, E + 2, size=(50, 3)).astype(np.int32)   # some ids outside [0, E)
+    sid, off = oracle.moe_align(ids, E)
+    flat = ids.reshape(-1)
+    want, offs = [], [0]
+    for e in range(E):                      # one pass per expert, pairs in index order
+        want += [p for p in range(flat.size) if flat[p] == e]
+        offs.append(len(want))
+    assert sid.tolist() == want and off.tolist() == offs
+    assert sid.dtype == np.int32 and off.dtype == np.int32
+
+
+def test_silu_mul_against_float64_on_every_fp16_gate():
+    """Every finite fp16 gate value g with up u: fp16(silu(g) * u) against the
+    float64 value rounded once; the fp32 steps may differ by one fp16 ulp
+    (double rounding), rarely.  The gate is the first half: g = 0 gives 0
+    whatever u, u = 0 gives 0 whatever g."""
+    bits = np.arange(0, 1 << 16, dtype=np.uint16)
+    g = bits.view(np.float16)
+    g = g[np.isfinite(g)]
+    for u_val in (1.0, -0.3740234375, 7.5):
+        h = np.stack([g, np.full_like(g, u_val)], axis=1)
+        got = oracle.silu_mul(h)[:, 0]
+        x = g.astype(np.float64)
+        with np.errstate(over="ignore"):
+            ref = (x / (1.0 + np.exp(-x)) * u_val).astype(np.float16)
+        d = np.abs(got.view(np.int16).astype(np.int32) - ref.view(np.int16).astype(np.int32))
+        assert (d <= 1).all() and (d == 0).mean() > 0.999, (u_val, int(d.max()), (d > 0).sum())
+    h = np.array([[0.0, 0.0, 3.0, -2.0], [1.5, -4.0, 0.0, 0.0]], dtype=np.float16)
+    out = oracle.silu_mul(h)
+    assert out[0].tolist() == [0.0, 0.0] and out[1].tolist() == [0.0, 0.0]
+
+
+def _moe_weights(E, H, I, g13, g2, rng):
+    def w(K, N, G):
+        packed = rng.integers(0, 256, size=(E, K, N // 2), dtype=np.uint8)
+        scales = (rng.random((E, K // G, N)) * 9e-3 + 1e-3).astype(np.float16)
+        zeros = rng.integers(0, 256, size=(E, K // G, N // 2), dtype=np.uint8)
+        return packed, scales, zeros
+    return w(H, 2 * I, g13) + w(I, H, g2)
+
+
+def test_moe_layer_matches_a_per_token_float64_loop():
+    """Token by token: rank the experts in float64, softmax over the top k,
+    and for each chosen expert run the feed-forward in float64 with the fp16
+    storage points of the layer (h, act, each weighted expert output, out).
+    A swapped gate/up half, a wrong token of a sorted row, a missing routing
+    weight or a wrong expert segment fails it."""
+    rng = np.random.default_rng(22)
+    T, E, k, H, I, g13, g2 = 9, 5, 2, 128, 64, 64, 64
+    X = rng.standard_normal((T, H)).astype(np.float16)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    W13, S13, Z13, W2, S2, Z2 = _moe_weights(E, H, I, g13, g2, rng)
+    got = oracle.fused_moe_w4a16(X, logits, W13, S13, Z13, W2, S2, Z2, k, g13, g2)
+    deq13 = [oracle.int4_dequant(W13[e], S13[e], Z13[e], g13).astype(np.float64) for e in range(E)]
+    deq2 = [oracle.int4_dequant(W2[e], S2[e], Z2[e], g2).astype(np.float64) for e in range(E)]
+    want = np.zeros((T, H), dtype=np.float64)
+    for t in range(T):
+        order = sorted(range(E), key=lambda e: (-float(logits[t, e]), e))[:k]
+        v = np.array([float(logits[t, e]) for e in order])
+        p = np.exp(v - v.max())
+        p /= p.sum()
+        acc = np.zeros(H)
+        for e, wt in zip(order, p):
+            h = (X[t].astype(np.float64) @ deq13[e]).astype(np.float16).astype(np.float64)
+            gte, up = h[:I], h[I:]
+            act = (gte / (1.0 + np.exp(-gte)) * up).astype(np.float16).astype(np.float64)
+            acc += (wt * (act @ deq2[e])).astype(np.float16).astype(np.float64)
+        want[t] = acc
+    np.testing.assert_allclose(got.astype(np.float64), want.astype(np.float16).astype(np.float64),
+                               rtol=1e-2, atol=1e-2)
+    assert np.abs(want).max() > 0.1   # not a trivially small layer
+
+
+def test_moe_layer_equivariance_under_token_and_expert_relabelling():
+    rng = np.random.default_rng(23)
+    T, E, k, H, I, g13, g2 = 12, 6, 3, 128, 64, 64, 64
+    X = rng.standard_normal((T, H)).astype(np.float16)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    W = _moe_weights(E, H, I, g13, g2, rng)
+    base = oracle.fused_moe_w4a16(X, logits, *W, k, g13, g2)
+    tp = rng.permutation(T)
+    out_t = oracle.fused_moe_w4a16(X[tp], logits[tp], *W, k, g13, g2)
+    np.testing.assert_allclose(out_t.astype(np.float32), base[tp].astype(np.float32), rtol=2e-3, atol=2e-3)
+    ep = rng.permutation(E)                  # expert e' = ep[e] is the old expert e
+    inv = np.argsort(ep)
+    out_e = oracle.fused_moe_w4a16(X, logits[:, inv], *[w[inv] for w in W], k, g13, g2)
+    np.testing.assert_allclose(out_e.astype(np.float32), base.astype(np.float32), rtol=2e-3, atol=2e-3)
+
+
+def test_moe_down_closed_form_and_combine_known_answer():
+    """Every dequantised W2 entry equal to s (q = z + 1) and act all ones: each
+    written row is fp16(w * I * s) exactly; unrouted rows stay unwritten.
+    Combine: slots summed in order in fp32, unrouted slots skipped."""
+    E, I, H, G = 2, 64, 16, 64
+    q = np.full((E, I, H), 4, dtype=np.uint8)
+    z = np.full((E, I // G, H), 3, dtype=np.uint8)
+    packed, zeros = oracle.pack_int4(q), oracle.pack_int4(z)
+    scales = np.full((E, I // G, H), 0.125, dtype=np.float16)
+    ids = np.array([[1, 0], [0, 9]], dtype=np.int32)          # pair 3 is routed nowhere
+    w = np.array([[0.25, 0.75], [0.5, 0.5]], dtype=np.float32)
+    sid, off = oracle.moe_align(ids, E)
+    assert sid.tolist() == [1, 2, 0] and off.tolist() == [0, 2, 3]
+    act = np.ones((3, I), dtype=np.float16)
+    Y, written = oracle.moe_down(act, sid, off, w, 4, packed, scales, zeros, G)
+    assert written.tolist() == [True, True, True, False]
+    assert Y[:3, 0].tolist() == [0.25 * 8, 0.75 * 8, 0.5 * 8] and (Y[3] == 0).all()
+    Yc = np.array([[1, 2], [3, 4], [5, 6], [7, 8]], dtype=np.float16)
+    out = oracle.moe_combine(Yc, ids, E)
+    assert out.tolist() == [[4, 6], [5, 6]]

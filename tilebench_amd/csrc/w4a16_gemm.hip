@@ -107,13 +107,45 @@ struct WRegs4 {
   uint32_t z;
 };
 
+// How a tile finds its A rows and what its epilogue writes.
+enum ARows { A_DIRECT = 0, A_GATHER = 1 };
+enum Epilogue { EPI_PLAIN = 0, EPI_SILU_MUL = 1, EPI_SCALE_SCATTER = 2 };
+
+// Row map of the MoE pipeline's tiles: tile row m is (token, slot) pair
+// ids[m]; the pair's token is ids[m] / topk and its routing weight w[ids[m]].
+struct RowMap {
+  const int* ids = nullptr;
+  const float* w = nullptr;
+  int topk = 1;
+  int pairs = 0;
+};
+
+// fp16 of an fp32 value that is already rounded: the empty asm keeps the
+// conversion from being folded into the preceding multiply (a mixed-precision
+// FMA would round the exact product once, not the fp32 product).
+__device__ __forceinline__ _Float16 h_of_rounded(float f) {
+  asm volatile("" : "+v"(f));
+  return (_Float16)f;
+}
+
 // One 256 x 256 tile: rows [m0, m_end) of A (A holds a_rows rows in all),
 // columns [n0, n0 + 256) of W (N columns), full K.  Shared by the dense kernel
-// and the grouped (MoE) kernel, which passes one expert's W / scales / zeros.
+// and the grouped (MoE) kernels, which pass one expert's W / scales / zeros.
+//   A_GATHER          : tile row m reads A row rm.ids[m] / rm.topk (a token of
+//                       the activations) instead of row m;
+//   EPI_SILU_MUL      : the tile's W columns are gate columns [n0/2, n0/2 + 128)
+//                       and up columns N/2 + [n0/2, n0/2 + 128) of W13 (N = 2I);
+//                       Y (row stride N/2) gets fp16(silu(g) * u) of the fp16
+//                       gate and up values, columns n0/2 ..;
+//   EPI_SCALE_SCATTER : the fp32 accumulator of row m is multiplied by
+//                       rm.w[rm.ids[m]] before rounding, and the row is stored
+//                       at row rm.ids[m] of Y.
+template <int AR, int EPI>
 __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _Float16* __restrict__ A,
                                              const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
                                              const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int a_rows,
-                                             int m0, int m_end, int n0, int N, int K, int group) {
+                                             int m0, int m_end, int n0, int N, int K, int group,
+                                             const RowMap rm = RowMap{}) {
   _Float16* const lds_a = lds;
   _Float16* const lds_b = lds + A_STAGES * A_STAGE;
   const Tile tile{m0, n0};
@@ -142,7 +174,12 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
       const int row = (wave * 4 + i) * 8 + lr;
       const int lc = (lane & 7) ^ ((row ^ (row >> 3)) & 7);
       const int m = tile.m0 + row;
-      a_off[i] = m < M ? ((uint32_t)m * (uint32_t)K + (uint32_t)lc * 8u) * 2u : OOB;
+      int src = m;
+      if (AR == A_GATHER && m < M) {
+        const int pid = rm.ids[m];
+        src = (unsigned)pid < (unsigned)rm.pairs ? pid / rm.topk : a_rows;  // a bad id reads zeros
+      }
+      a_off[i] = m < M && src < a_rows ? ((uint32_t)src * (uint32_t)K + (uint32_t)lc * 8u) * 2u : OOB;
     }
   }
   const uint32_t a_lds0 = (uint32_t)__builtin_amdgcn_readfirstlane(
@@ -150,11 +187,17 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
 
   // W: thread owns rows kq*4 .. kq*4+3 of the 64-row step, columns cg*8 .. +7.
   const int cg = t & 31, kq = t >> 5;
-  const int n = tile.n0 + cg * 8;
+  int n = tile.n0 + cg * 8;
+  bool n_ok = n < N;
+  if (EPI == EPI_SILU_MUL) {
+    const int half_cols = N / 2, a0 = tile.n0 / 2 + (cg & 15) * 8;  // activation column of this group
+    n = (cg < 16 ? 0 : half_cols) + a0;
+    n_ok = a0 < half_cols;
+  }
   const uint32_t w_row = (uint32_t)(N / 2);
-  const uint32_t w_off = n < N ? (uint32_t)(kq * 4) * w_row + (uint32_t)(n / 2) : OOB;
-  const uint32_t s_off = n < N ? (uint32_t)n * 2u : OOB;
-  const uint32_t z_off = n < N ? (uint32_t)(n / 2) : OOB;
+  const uint32_t w_off = n_ok ? (uint32_t)(kq * 4) * w_row + (uint32_t)(n / 2) : OOB;
+  const uint32_t s_off = n_ok ? (uint32_t)n * 2u : OOB;
+  const uint32_t z_off = n_ok ? (uint32_t)(n / 2) : OOB;
   int b_st[8];
 #pragma unroll
   for (int c = 0; c < 8; ++c) b_st[c] = swz2(cg * 8 + c, kq >> 1) + (kq & 1) * 4;
@@ -297,6 +340,15 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
   // Accumulator elements 4g .. 4g+3 of fragment (i, j) are row i*32 + lane%32,
   // columns j*32 + g*8 + (lane/32)*4 + 0..3 of the wave tile.
   _Float16* ct = lds;
+  float row_w[4] = {1.f, 1.f, 1.f, 1.f};
+  if (EPI == EPI_SCALE_SCATTER) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = tile.m0 + wm * 128 + i * 32 + (lane & 31);
+      const int pid = m < M ? rm.ids[m] : -1;
+      row_w[i] = (unsigned)pid < (unsigned)rm.pairs ? rm.w[pid] : 0.f;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -305,20 +357,60 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
       for (int g = 0; g < 4; ++g) {
         const int row = wm * 128 + i * 32 + (lane & 31);
         const int col = wn * 64 + j * 32 + g * 8 + (lane >> 5) * 4;
+        _Float16 h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          h[e] = EPI == EPI_SCALE_SCATTER ? h_of_rounded(acc[i][j][4 * g + e] * row_w[i]) : (_Float16)acc[i][j][4 * g + e];
         u32x2v v;
-        v[0] = as_u32(f16x2{(_Float16)acc[i][j][4 * g], (_Float16)acc[i][j][4 * g + 1]});
-        v[1] = as_u32(f16x2{(_Float16)acc[i][j][4 * g + 2], (_Float16)acc[i][j][4 * g + 3]});
+        v[0] = as_u32(f16x2{h[0], h[1]});
+        v[1] = as_u32(f16x2{h[2], h[3]});
         *reinterpret_cast<u32x2v*>(ct + row * C_STRIDE + col) = v;
       }
   __syncthreads();
   const int rows = min(BM, M - tile.m0);
+  if (EPI == EPI_SILU_MUL) {
+    // 128 activation columns per tile: gate in staged columns 0..127, up in 128..255
+    const int half_cols = N / 2, a0 = tile.n0 / 2;
+    const int acols = min(BN / 2, half_cols - a0);
+#pragma unroll 4
+    for (int idx = t; idx < BM * (BN / 16); idx += T4) {
+      const int row = idx >> 4, ch = idx & 15;
+      if (row < rows && ch * 8 < acols) {
+        const u32x4 gv = *reinterpret_cast<const u32x4*>(ct + row * C_STRIDE + ch * 8);
+        const u32x4 uv = *reinterpret_cast<const u32x4*>(ct + row * C_STRIDE + BN / 2 + ch * 8);
+        u32x4 o;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f16x2 g2 = as_h2(gv[q]), u2 = as_h2(uv[q]);
+          _Float16 r[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const float g = (float)g2[e], u = (float)u2[e];
+            float sg = 1.0f + expf(-g);
+            asm volatile("" : "+v"(sg));
+            const float si = g / sg;
+            r[e] = h_of_rounded(si * u);
+          }
+          o[q] = as_u32(f16x2{r[0], r[1]});
+        }
+        *reinterpret_cast<u32x4*>(Y + (int64_t)(tile.m0 + row) * half_cols + a0 + ch * 8) = o;
+      }
+    }
+    return;
+  }
   const int cols = min(BN, N - tile.n0);
 #pragma unroll 4
   for (int idx = t; idx < BM * (BN / 8); idx += T4) {
     const int row = idx >> 5, ch = idx & 31;
     if (row < rows && ch * 8 < cols) {
       const u32x4 v = *reinterpret_cast<const u32x4*>(ct + row * C_STRIDE + ch * 8);
-      *reinterpret_cast<u32x4*>(Y + (int64_t)(tile.m0 + row) * N + tile.n0 + ch * 8) = v;
+      int64_t dst = tile.m0 + row;
+      if (EPI == EPI_SCALE_SCATTER) {
+        const int pid = rm.ids[tile.m0 + row];
+        if ((unsigned)pid >= (unsigned)rm.pairs) continue;
+        dst = pid;
+      }
+      *reinterpret_cast<u32x4*>(Y + dst * N + tile.n0 + ch * 8) = v;
     }
   }
 }
@@ -329,7 +421,35 @@ __global__ void __launch_bounds__(T4, 1)
                   int tiles_m, int tiles_n) {
   extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
   const Tile tile = tile_of_block(tiles_m, tiles_n);
-  prefill_tile(lds, A, W, S, Z, Y, M, tile.m0, M, tile.n0, N, K, group);
+  prefill_tile<A_DIRECT, EPI_PLAIN>(lds, A, W, S, Z, Y, M, tile.m0, M, tile.n0, N, K, group);
+}
+
+// Expert and row range of grouped tile row mt: rows offsets[e] .. offsets[e+1]
+// of the row space (R rows) use expert e, cut into 256-row tiles.  Offsets are
+// clamped to [0, R] so that malformed ones never address rows outside A / Y.
+// Returns false past the last tile.
+__device__ __forceinline__ bool grouped_tile(const int* __restrict__ offsets, int experts, int R, int mt, int& e,
+                                             int& m0, int& m_end) {
+  int seen = 0;
+  for (int x = 0; x < experts; ++x) {
+    const int lo = min(max(offsets[x], 0), R), hi = min(max(offsets[x + 1], lo), R);
+    const int cnt = (hi - lo + BM - 1) / BM;
+    if (mt < seen + cnt) {
+      e = x;
+      m0 = lo + (mt - seen) * BM;
+      m_end = hi;
+      return true;
+    }
+    seen += cnt;
+  }
+  return false;
+}
+
+__device__ __forceinline__ int grouped_block_id() {
+  const int nb = gridDim.x;
+  int bid = blockIdx.x;
+  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  return bid;
 }
 
 // Grouped (MoE) variant: rows offsets[e] .. offsets[e+1] of A use expert e's
@@ -343,27 +463,59 @@ __global__ void __launch_bounds__(T4, 1)
                   const uint8_t* __restrict__ Z, const int* __restrict__ offsets, _Float16* __restrict__ Y, int R,
                   int experts, int N, int K, int group, int tiles_n) {
   extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
-  const int nb = gridDim.x;
-  int bid = blockIdx.x;
-  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  const int bid = grouped_block_id();
   const int mt = bid / tiles_n, nt = bid - mt * tiles_n;
-  int e = -1, m0 = 0, m_end = 0;
-  int seen = 0;
-  for (int x = 0; x < experts; ++x) {
-    // clamped to [0, R] so that malformed offsets can never address rows outside A / Y
-    const int lo = min(max(offsets[x], 0), R), hi = min(max(offsets[x + 1], lo), R);
-    const int cnt = (hi - lo + BM - 1) / BM;
-    if (mt < seen + cnt) {
-      e = x;
-      m0 = lo + (mt - seen) * BM;
-      m_end = hi;
-      break;
-    }
-    seen += cnt;
-  }
-  if (e < 0) return;  // beyond the last tile: uniform across the block
+  int e = 0, m0 = 0, m_end = 0;
+  if (!grouped_tile(offsets, experts, R, mt, e, m0, m_end)) return;  // beyond the last tile: uniform
   const int64_t wstride = (int64_t)K * (N / 2), sstride = (int64_t)(K / group) * N, zstride = (int64_t)(K / group) * (N / 2);
-  prefill_tile(lds, A, W + e * wstride, S + e * sstride, Z + e * zstride, Y, R, m0, m_end, nt * BN, N, K, group);
+  prefill_tile<A_DIRECT, EPI_PLAIN>(lds, A, W + e * wstride, S + e * sstride, Z + e * zstride, Y, R, m0, m_end,
+                                    nt * BN, N, K, group);
+}
+
+// MoE gate/up projection: rows of the pair space (sorted by expert, offsets[e]
+// .. offsets[e+1] for expert e) gather their token's activation row X[ids[m] /
+// topk], multiply by expert e's W13 [K, 2I] and write fp16(silu(gate) * up),
+// I columns per row, in the same sorted row order.  128 output columns per tile.
+__global__ void __launch_bounds__(T4, 1)
+    moe_gate_up(const _Float16* __restrict__ X, const int* __restrict__ ids, const int* __restrict__ offsets,
+                const uint8_t* __restrict__ W, const _Float16* __restrict__ S, const uint8_t* __restrict__ Z,
+                _Float16* __restrict__ act, int tokens, int topk, int pairs, int experts, int I, int K, int group,
+                int tiles_n) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+  const int bid = grouped_block_id();
+  const int mt = bid / tiles_n, nt = bid - mt * tiles_n;
+  int e = 0, m0 = 0, m_end = 0;
+  if (!grouped_tile(offsets, experts, pairs, mt, e, m0, m_end)) return;
+  const int N = 2 * I;
+  const int64_t wstride = (int64_t)K * I, sstride = (int64_t)(K / group) * N, zstride = (int64_t)(K / group) * I;
+  RowMap rm;
+  rm.ids = ids;
+  rm.topk = topk;
+  rm.pairs = pairs;
+  prefill_tile<A_GATHER, EPI_SILU_MUL>(lds, X, W + e * wstride, S + e * sstride, Z + e * zstride, act, tokens, m0,
+                                       m_end, nt * BN, N, K, group, rm);
+}
+
+// MoE down projection: sorted activation rows times expert e's W2 [I, H]; row m
+// is scaled by its pair's routing weight w[ids[m]] in fp32 and stored, as fp16,
+// at row ids[m] of Y [pairs, H] (token-major: pair t * topk + j).
+__global__ void __launch_bounds__(T4, 1)
+    moe_down(const _Float16* __restrict__ act, const int* __restrict__ ids, const int* __restrict__ offsets,
+             const float* __restrict__ w, const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
+             const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int pairs, int experts, int H, int I,
+             int group, int tiles_n) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+  const int bid = grouped_block_id();
+  const int mt = bid / tiles_n, nt = bid - mt * tiles_n;
+  int e = 0, m0 = 0, m_end = 0;
+  if (!grouped_tile(offsets, experts, pairs, mt, e, m0, m_end)) return;
+  const int64_t wstride = (int64_t)I * (H / 2), sstride = (int64_t)(I / group) * H, zstride = (int64_t)(I / group) * (H / 2);
+  RowMap rm;
+  rm.ids = ids;
+  rm.w = w;
+  rm.pairs = pairs;
+  prefill_tile<A_DIRECT, EPI_SCALE_SCATTER>(lds, act, W + e * wstride, S + e * sstride, Z + e * zstride, Y, pairs,
+                                            m0, m_end, nt * BN, H, I, group, rm);
 }
 
 // ---------------------------------------------------------------------------
@@ -696,4 +848,88 @@ extern "C" tb_status tb_moe_w4a16_grouped_gemm(const uint16_t* A, const uint8_t*
                      reinterpret_cast<const _Float16*>(A), W, reinterpret_cast<const _Float16*>(scales), zeros, offsets,
                      reinterpret_cast<_Float16*>(Y), (int)R, (int)experts, (int)N, (int)K, (int)group, (int)tiles_n);
   return tb::launch_status("tb_moe_w4a16_grouped_gemm");
+}
+
+namespace {
+// Reserve the tile routine's 160 KiB of dynamic LDS for a kernel, once.
+template <typename F>
+tb_status reserve_lds(F* kernel, bool& done, const char* what) {
+  if (!done) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)tb::w4a16::LDS4_BYTES) != hipSuccess) {
+      tb::set_error("%s: cannot reserve %zu bytes of LDS", what, tb::w4a16::LDS4_BYTES);
+      return TB_E_HIP;
+    }
+    done = true;
+  }
+  return TB_OK;
+}
+}  // namespace
+
+extern "C" tb_status tb_moe_w4a16_gate_up(const uint16_t* X, const int32_t* sorted_ids, const int32_t* offsets,
+                                          const uint8_t* W13, const uint16_t* S13, const uint8_t* Z13, uint16_t* act,
+                                          int64_t tokens, int64_t topk, int64_t experts, int64_t H, int64_t I,
+                                          int64_t group, hipStream_t stream) {
+  using namespace tb::w4a16;
+  const char* fn = "tb_moe_w4a16_gate_up";
+  TB_CHECK_ARG(X && sorted_ids && offsets && W13 && S13 && Z13 && act, "%s: null pointer", fn);
+  TB_CHECK_ARG(tokens > 0 && topk > 0 && experts > 0 && H > 0 && I > 0 && group > 0, "%s: sizes must be positive", fn);
+  TB_CHECK_ARG(experts <= 4096 && topk <= experts, "%s: need topk <= experts <= 4096", fn);
+  const int64_t pairs = tokens * topk;
+  TB_CHECK_ARG(pairs < (1ll << 31), "%s: tokens * topk must be < 2^31", fn);
+  TB_CHECK_ARG(I % 8 == 0, "%s: I must be a multiple of 8 (got %lld)", fn, (long long)I);
+  TB_CHECK_ARG(H % BK == 0 && group % BK == 0 && H % group == 0,
+               "%s: need H %% 64 == 0, group %% 64 == 0 and H %% group == 0 (H=%lld group=%lld)", fn, (long long)H,
+               (long long)group);
+  TB_CHECK_ARG(tokens * H * 2 < (1ll << 32) && H * I < (1ll << 31) && pairs * I * 2 < (1ll << 62),
+               "%s: X must be < 4 GiB and one expert's W13 < 2 GiB", fn);
+  TB_CHECK_ALIGN(X, 16, "X");
+  TB_CHECK_ALIGN(W13, 4, "W13");
+  TB_CHECK_ALIGN(S13, 16, "S13");
+  TB_CHECK_ALIGN(Z13, 4, "Z13");
+  TB_CHECK_ALIGN(act, 16, "act");
+  static bool lds_ok = false;
+  if (tb_status st = reserve_lds(&moe_gate_up, lds_ok, fn)) return st;
+  const int64_t tiles_n = (I + BN / 2 - 1) / (BN / 2);
+  const int64_t tile_rows = (pairs + BM - 1) / BM + experts;
+  const int64_t blocks = tile_rows * tiles_n;
+  TB_CHECK_ARG(blocks < (1ll << 31), "%s: problem too large", fn);
+  hipLaunchKernelGGL(moe_gate_up, dim3((unsigned)blocks), dim3(T4), LDS4_BYTES, stream,
+                     reinterpret_cast<const _Float16*>(X), sorted_ids, offsets, W13,
+                     reinterpret_cast<const _Float16*>(S13), Z13, reinterpret_cast<_Float16*>(act), (int)tokens,
+                     (int)topk, (int)pairs, (int)experts, (int)I, (int)H, (int)group, (int)tiles_n);
+  return tb::launch_status(fn);
+}
+
+extern "C" tb_status tb_moe_w4a16_down(const uint16_t* act, const int32_t* sorted_ids, const int32_t* offsets,
+                                       const float* topk_weights, const uint8_t* W2, const uint16_t* S2,
+                                       const uint8_t* Z2, uint16_t* Y, int64_t pairs, int64_t experts, int64_t I,
+                                       int64_t H, int64_t group, hipStream_t stream) {
+  using namespace tb::w4a16;
+  const char* fn = "tb_moe_w4a16_down";
+  TB_CHECK_ARG(act && sorted_ids && offsets && topk_weights && W2 && S2 && Z2 && Y, "%s: null pointer", fn);
+  TB_CHECK_ARG(pairs > 0 && experts > 0 && H > 0 && I > 0 && group > 0, "%s: sizes must be positive", fn);
+  TB_CHECK_ARG(experts <= 4096 && pairs < (1ll << 31), "%s: need experts <= 4096 and pairs < 2^31", fn);
+  TB_CHECK_ARG(H % 8 == 0, "%s: H must be a multiple of 8 (got %lld)", fn, (long long)H);
+  TB_CHECK_ARG(I % BK == 0 && group % BK == 0 && I % group == 0,
+               "%s: need I %% 64 == 0, group %% 64 == 0 and I %% group == 0 (I=%lld group=%lld)", fn, (long long)I,
+               (long long)group);
+  TB_CHECK_ARG(pairs * I * 2 < (1ll << 32) && I * (H / 2) < (1ll << 31),
+               "%s: act must be < 4 GiB and one expert's W2 < 2 GiB", fn);
+  TB_CHECK_ALIGN(act, 16, "act");
+  TB_CHECK_ALIGN(W2, 4, "W2");
+  TB_CHECK_ALIGN(S2, 16, "S2");
+  TB_CHECK_ALIGN(Z2, 4, "Z2");
+  TB_CHECK_ALIGN(Y, 16, "Y");
+  static bool lds_ok = false;
+  if (tb_status st = reserve_lds(&moe_down, lds_ok, fn)) return st;
+  const int64_t tiles_n = (H + BN - 1) / BN;
+  const int64_t tile_rows = (pairs + BM - 1) / BM + experts;
+  const int64_t blocks = tile_rows * tiles_n;
+  TB_CHECK_ARG(blocks < (1ll << 31), "%s: problem too large", fn);
+  hipLaunchKernelGGL(moe_down, dim3((unsigned)blocks), dim3(T4), LDS4_BYTES, stream,
+                     reinterpret_cast<const _Float16*>(act), sorted_ids, offsets, topk_weights, W2,
+                     reinterpret_cast<const _Float16*>(S2), Z2, reinterpret_cast<_Float16*>(Y), (int)pairs,
+                     (int)experts, (int)H, (int)I, (int)group, (int)tiles_n);
+  return tb::launch_status(fn);
 }

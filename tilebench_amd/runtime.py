@@ -38,6 +38,12 @@ SIGNATURES: dict[str, list] = {
     "tb_w4a16_gemm": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p],
     "tb_w4a16_workspace_size": [_c_i64, _c_i64, _c_i64, _c_i64, ctypes.POINTER(_c_i64)],
     "tb_moe_w4a16_grouped_gemm": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p],
+    "tb_moe_align": [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p],
+    "tb_moe_w4a16_gate_up": [_c_p] * 7 + [_c_i64] * 6 + [_c_p],
+    "tb_moe_w4a16_down": [_c_p] * 8 + [_c_i64] * 5 + [_c_p],
+    "tb_moe_combine": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p],
+    "tb_fused_moe_w4a16_workspace_size": [_c_i64] * 5 + [ctypes.POINTER(_c_i64)],
+    "tb_fused_moe_w4a16": [_c_p] * 9 + [_c_i64] * 7 + [_c_p, _c_i64, _c_p],
     "tb_fp8_scaled_gemm": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p],
     "tb_weight_dequant": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p],
     "tb_dequantize_rowwise": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_p],
