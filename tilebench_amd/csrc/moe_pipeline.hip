@@ -14,48 +14,64 @@
 //
 // The align kernel runs one block per expert.  Every block reads the whole id
 // list twice: first counting the pairs of lower experts (its first row) and of
-// its own, then compacting its own pairs in list order (a block-wide prefix
-// over per-thread match counts).  No atomics, and the result does not depend
-// on scheduling.
+// its own, then compacting its own pairs in list order.  No atomics, and the
+// result does not depend on scheduling.
 #include "tb_common.h"
 
 namespace tb {
 namespace moe {
 
 constexpr int ALIGN_THREADS = 1024, ALIGN_WAVES = ALIGN_THREADS / 64;
+constexpr int IDS_PER_LANE = 16;  // ids a lane takes per step: 64 contiguous bytes
+constexpr int WAVE_STEP = 64 * IDS_PER_LANE;
 
-__device__ __forceinline__ void load4(const int* __restrict__ ids, int64_t q, int64_t pairs, bool vec, int (&v)[4]) {
-  const int64_t i0 = q * 4;
-  if (vec && i0 + 3 < pairs) {
-    const int4 x = *reinterpret_cast<const int4*>(ids + i0);
-    v[0] = x.x;
-    v[1] = x.y;
-    v[2] = x.z;
-    v[3] = x.w;
+// Ids [i0, i0 + 16) of this lane (ids past `end` read as -1): four 16-byte
+// loads when the list is 16-byte aligned.
+__device__ __forceinline__ void load16(const int* __restrict__ ids, int64_t i0, int64_t end, bool vec,
+                                       int (&v)[IDS_PER_LANE]) {
+  if (vec && i0 + IDS_PER_LANE <= end) {
+#pragma unroll
+    for (int u = 0; u < IDS_PER_LANE / 4; ++u) {
+      const int4 x = *reinterpret_cast<const int4*>(ids + i0 + 4 * u);
+      v[4 * u] = x.x;
+      v[4 * u + 1] = x.y;
+      v[4 * u + 2] = x.z;
+      v[4 * u + 3] = x.w;
+    }
   } else {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = i0 + u < pairs ? ids[i0 + u] : -1;
+    for (int u = 0; u < IDS_PER_LANE; ++u) v[u] = i0 + u < end ? ids[i0 + u] : -1;
   }
 }
 
+// Block e places expert e's pairs.  Wavefront w owns slice w of the id list
+// (contiguous, so slice order is list order): it counts the ids of lower
+// experts and of expert e in its slice, the block adds the 16 slice counts,
+// and each wavefront then compacts its own slice from its slice's base with
+// a wave-level prefix sum only.  Every step prefetches the next step's ids.
 __global__ void __launch_bounds__(ALIGN_THREADS)
     moe_align_kernel(const int* __restrict__ ids, int64_t pairs, int experts, int* __restrict__ sorted,
                      int* __restrict__ offsets, bool vec) {
   __shared__ int red[2][ALIGN_WAVES];
-  __shared__ int wave_base[ALIGN_WAVES];
   const int e = blockIdx.x;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int64_t quads = (pairs + 3) / 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t slice = (pairs + ALIGN_WAVES * WAVE_STEP - 1) / (ALIGN_WAVES * WAVE_STEP) * WAVE_STEP;
+  const int64_t s_begin = min(pairs, slice * wave), s_end = min(pairs, s_begin + slice);
 
-  // pass 1: pairs of lower experts and of this one
+  // pass 1: ids of lower experts and of this one in the slice
   int below = 0, mine = 0;
-  for (int64_t q = t; q < quads; q += ALIGN_THREADS) {
-    int v[4];
-    load4(ids, q, pairs, vec, v);
+  {
+    int cur[IDS_PER_LANE], nxt[IDS_PER_LANE];
+    load16(ids, s_begin + lane * IDS_PER_LANE, s_end, vec, cur);
+    for (int64_t b = s_begin; b < s_end; b += WAVE_STEP) {
+      if (b + WAVE_STEP < s_end) load16(ids, b + WAVE_STEP + lane * IDS_PER_LANE, s_end, vec, nxt);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      below += (unsigned)v[u] < (unsigned)e;  // ids outside [0, experts) are routed nowhere
-      mine += v[u] == e;
+      for (int u = 0; u < IDS_PER_LANE; ++u) {
+        below += (unsigned)cur[u] < (unsigned)e;  // ids outside [0, experts) are routed nowhere
+        mine += cur[u] == e;
+      }
+#pragma unroll
+      for (int u = 0; u < IDS_PER_LANE; ++u) cur[u] = nxt[u];
     }
   }
 #pragma unroll
@@ -68,47 +84,42 @@ __global__ void __launch_bounds__(ALIGN_THREADS)
     red[1][wave] = mine;
   }
   __syncthreads();
-  int first = 0, count = 0;
+  int first = 0, count = 0, before = 0;
 #pragma unroll
   for (int w = 0; w < ALIGN_WAVES; ++w) {
     first += red[0][w];
     count += red[1][w];
+    before += w < wave ? red[1][w] : 0;
   }
-  if (t == 0) {
+  if (threadIdx.x == 0) {
     offsets[e] = first;
     if (e == experts - 1) offsets[experts] = first + count;
   }
+  if (red[1][wave] == 0) return;  // nothing of expert e in this slice (uniform per wavefront)
 
-  // pass 2: stable compaction, 4096 ids per round
-  int base = first;
-  for (int64_t q0 = 0; q0 < quads; q0 += ALIGN_THREADS) {
-    const int64_t q = q0 + t;
-    int v[4] = {-1, -1, -1, -1};
-    if (q < quads) load4(ids, q, pairs, vec, v);
+  // pass 2: stable compaction of the slice
+  int pos = first + before;
+  int cur[IDS_PER_LANE], nxt[IDS_PER_LANE];
+  load16(ids, s_begin + lane * IDS_PER_LANE, s_end, vec, cur);
+  for (int64_t b = s_begin; b < s_end; b += WAVE_STEP) {
+    if (b + WAVE_STEP < s_end) load16(ids, b + WAVE_STEP + lane * IDS_PER_LANE, s_end, vec, nxt);
     int c = 0;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) c += v[u] == e;
-    int incl = c;  // inclusive prefix over the wave's lanes
+    for (int u = 0; u < IDS_PER_LANE; ++u) c += cur[u] == e;
+    int incl = c;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
       const int o = __shfl_up(incl, d);
       if (lane >= d) incl += o;
     }
-    __syncthreads();  // wave_base of the previous round has been read
-    if (lane == 63) wave_base[wave] = incl;
-    __syncthreads();
-    int before = 0, total = 0;
+    int p = pos + incl - c;
+    const int64_t i0 = b + lane * IDS_PER_LANE;
 #pragma unroll
-    for (int w = 0; w < ALIGN_WAVES; ++w) {
-      const int x = wave_base[w];
-      before += w < wave ? x : 0;
-      total += x;
-    }
-    int pos = base + before + incl - c;
+    for (int u = 0; u < IDS_PER_LANE; ++u)
+      if (cur[u] == e) sorted[p++] = (int)(i0 + u);
+    pos += __shfl(incl, 63);
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (v[u] == e) sorted[pos++] = (int)(q * 4 + u);
-    base += total;
+    for (int u = 0; u < IDS_PER_LANE; ++u) cur[u] = nxt[u];
   }
 }
 
