@@ -54,6 +54,25 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int GROUP_M = 4;  // tile rows per ordering group
 
+// (1024 + q) half2 pairs of one packed dword in the order columns (0,2), (4,6),
+// (1,3), (5,7): one byte permute per pair takes two codes from the masked
+// nibble word and the 0x64 high bytes from a constant word, so no OR is needed.
+__device__ __forceinline__ void unpack8x(uint32_t w, f16x2 (&h)[4]) {
+  const uint32_t even = w & 0x0F0F0F0Fu;         // columns 0, 2, 4, 6
+  const uint32_t odd = (w >> 4) & 0x0F0F0F0Fu;   // columns 1, 3, 5, 7
+  const uint32_t c64 = 0x64646464u;
+  h[0] = as_h2(perm(c64, even, 0x04010400u));
+  h[1] = as_h2(perm(c64, even, 0x04030402u));
+  h[2] = as_h2(perm(c64, odd, 0x04010400u));
+  h[3] = as_h2(perm(c64, odd, 0x04030402u));
+}
+// Scale half2 pairs (0,1), (2,3), (4,5), (6,7) reordered to unpack8x's order.
+__device__ __forceinline__ void scales_x(const u32x4 s, f16x2 (&h)[4]) {
+  h[0] = as_h2(perm(s[1], s[0], 0x05040100u));
+  h[1] = as_h2(perm(s[3], s[2], 0x05040100u));
+  h[2] = as_h2(perm(s[1], s[0], 0x07060302u));
+  h[3] = as_h2(perm(s[3], s[2], 0x07060302u));
+}
 // (1024 + q) half2 pairs of one packed dword: columns (0,1), (2,3), (4,5), (6,7).
 __device__ __forceinline__ void unpack8(uint32_t w, f16x2 (&h)[4]) {
   const uint32_t even = w & 0x0F0F0F0Fu;
@@ -563,12 +582,17 @@ __global__ void __launch_bounds__(T4, 1)
 // wavefronts owns a 256-column slab and one of S contiguous K ranges, and the
 // grid never holds more blocks than the device has CUs (one block fills a CU),
 // so every block starts at once.  Each wavefront streams its own contiguous
-// run of 32-row units with a four-unit prefetch; per unit a lane loads an
-// 8 x 16 int4 block (eight 8-byte row loads; 16 lanes side by side cover a
-// full 128-byte line of a row), dequantises it exactly as the prefill kernel
-// does, pairs consecutive rows of a column with one byte permute, and feeds
-// sixteen v_mfma_f32_16x16x32_f16 (A rows >= M are zero): fragment f holds
-// columns 16c + f, c = lane % 16.  The eight wave partials are summed in LDS in
+// run of 32-row units, the next unit's loads issued as soon as a unit has been
+// consumed (one unit in flight per wavefront: the chip's loads then arrive
+// early enough for compute to overlap them; deeper prefetch measured slower).
+// Per unit a lane loads an 8 x 16 int4 block (eight 8-byte row loads; 16 lanes
+// side by side cover a full 128-byte line of a row) with its group's scales and
+// zero-points, all buffer loads whose offsets are out of range (zeros, no
+// traffic) where a row, column or unit does not exist, so no load sits behind
+// a branch and the compiler's wait before a unit covers only that unit.  It
+// dequantises exactly as the prefill kernel does, pairs consecutive rows of a
+// column with one byte permute, and feeds sixteen v_mfma_f32_16x16x32_f16
+// (A rows >= M are zero): fragment f holds columns 16c + f, c = lane % 16.  The eight wave partials are summed in LDS in
 // a fixed order, so results are reproducible bit for bit.
 // Across the S blocks of a slab the reduction is a serial split-K: each block
 // writes its fp32 partial through to the device-coherent level, then bumps the
@@ -576,7 +600,7 @@ __global__ void __launch_bounds__(T4, 1)
 // (all loads in flight at once), adds them in slot order (deterministic),
 // writes fp16 Y and puts the counter back to zero, so the workspace is ready
 // for the next call without any clearing.
-constexpr int DEC_COLS = 256, DEC_THREADS = 512, DEC_WAVES = 8, DEC_UNIT = 32, DEC_DEPTH = 4, DEC_MAX_SPLITS = 16;
+constexpr int DEC_COLS = 256, DEC_THREADS = 512, DEC_WAVES = 8, DEC_UNIT = 32, DEC_DEPTH = 1, DEC_MAX_SPLITS = 16;
 constexpr int AUX_SC1 = 16;  // buffer cache policy: coherent across the XCDs
 // Workspace layout, the same for every shape so that calls of different shapes
 // can share one buffer: [DEC_MAX_SLABS int32 arrival counters][fp32 partials].
@@ -589,8 +613,11 @@ typedef float f32x4d __attribute__((ext_vector_type(4)));
 struct DecUnit {
   u32x2 w[8];  // rows kg*8 + r, columns 16c .. 16c + 15
   u32x4 a;     // A row lane % 16, k = kg*8 .. +7
+  u32x4 s0, s1;  // scales of the unit's group, columns 16c .. 16c + 15
+  uint32_t z0, z1;
 };
 
+template <bool TAIL>
 __global__ void __launch_bounds__(DEC_THREADS)
     w4a16_decode(const _Float16* __restrict__ A, const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
                  const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, float* __restrict__ partials,
@@ -607,46 +634,56 @@ __global__ void __launch_bounds__(DEC_THREADS)
   const int units = K / DEC_UNIT;
   const int u_begin = (int)((int64_t)units * split / splits), u_end = (int)((int64_t)units * (split + 1) / splits);
   const int bu = u_end - u_begin;
-  const int w_begin = u_begin + (int)((int64_t)bu * wave / DEC_WAVES);
-  const int w_end = u_begin + (int)((int64_t)bu * (wave + 1) / DEC_WAVES);
-  const int64_t half_n = N >> 1;
+  const int w_begin = __builtin_amdgcn_readfirstlane(u_begin + (int)((int64_t)bu * wave / DEC_WAVES));
+  const int w_end = __builtin_amdgcn_readfirstlane(u_begin + (int)((int64_t)bu * (wave + 1) / DEC_WAVES));
+  const uint32_t half_n = (uint32_t)(N >> 1);
   const int arow = lane & 15;
+
+  // Every load is a buffer load with a per-lane offset that is out of range
+  // (reads zeros) where the row or column does not exist: no branches around
+  // loads, so the compiler's wait before each unit covers only that unit.
+  const rsrc_t rw = make_rsrc(W, (uint32_t)K * half_n);
+  const rsrc_t ra = make_rsrc(A, (uint32_t)M * (uint32_t)K * 2u);
+  const rsrc_t rs = make_rsrc(S, (uint32_t)(K / group) * (uint32_t)N * 2u);
+  const rsrc_t rz = make_rsrc(Z, (uint32_t)(K / group) * half_n);
+  const uint32_t w_off = col_full ? (uint32_t)(kg * 8) * half_n + (uint32_t)(n >> 1) : OOB;
+  const uint32_t w_tail = (TAIL && col_ok && !col_full) ? (uint32_t)(kg * 8) * half_n + (uint32_t)(n >> 1) : OOB;
+  const uint32_t a_off = arow < M ? ((uint32_t)arow * (uint32_t)K + (uint32_t)(kg * 8)) * 2u : OOB;
+  const uint32_t s_off0 = col_ok ? (uint32_t)n * 2u : OOB, s_off1 = col_full ? (uint32_t)(n + 8) * 2u : OOB;
+  const uint32_t z_off0 = col_ok ? (uint32_t)(n >> 1) : OOB, z_off1 = col_full ? (uint32_t)(n >> 1) + 4u : OOB;
+  constexpr int NT = 2;  // nontemporal: the weights are read once
 
   f32x4d acc[16];
 #pragma unroll
   for (int f = 0; f < 16; ++f) acc[f] = f32x4d{};
 
+  // A unit past the wavefront's range is still issued, with an out-of-range
+  // offset (no memory traffic, zeros): the loop has no branch around a load.
   auto load_unit = [&](DecUnit& d, int u) {
-    const int k = u * DEC_UNIT + kg * 8;
-    const uint8_t* wp = W + (int64_t)k * half_n + (n >> 1);
+    const bool live = u < w_end;
+    const uint32_t kw = live ? (uint32_t)(u * DEC_UNIT) * half_n : OOB;
+    const int g = live ? (u * DEC_UNIT) / group : 0;
+    const uint32_t ks = live ? (uint32_t)g * (uint32_t)N * 2u : OOB, kz = live ? (uint32_t)g * half_n : OOB;
+    d.s0 = __builtin_amdgcn_raw_buffer_load_b128(rs, s_off0, ks, 0);
+    d.s1 = __builtin_amdgcn_raw_buffer_load_b128(rs, s_off1, ks, 0);
+    d.z0 = __builtin_amdgcn_raw_buffer_load_b32(rz, z_off0, kz, 0);
+    d.z1 = __builtin_amdgcn_raw_buffer_load_b32(rz, z_off1, kz, 0);
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
-      const uint8_t* row = wp + (int64_t)r * half_n;
-      if (col_full) d.w[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(row));
-      else d.w[r] = u32x2{col_ok ? __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(row)) : 0u, 0u};
-    }
-    d.a = arow < M ? *reinterpret_cast<const u32x4*>(A + (int64_t)arow * K + k) : u32x4{0u, 0u, 0u, 0u};
-  };
-  int cur_g = -1;
-  f16x2 zh[2][4], sh[2][4];
-  auto compute_unit = [&](const DecUnit& d, int u) {
-    const int g = (u * DEC_UNIT) / group;
-    if (g != cur_g) {
-      cur_g = g;
-      const _Float16* sp = S + (int64_t)g * N + n;
-      const uint8_t* zp = Z + (int64_t)g * half_n + (n >> 1);
-      const u32x4 s0 = col_ok ? *reinterpret_cast<const u32x4*>(sp) : u32x4{0u, 0u, 0u, 0u};
-      const u32x4 s1 = col_full ? *reinterpret_cast<const u32x4*>(sp + 8) : u32x4{0u, 0u, 0u, 0u};
-      const uint32_t z0 = col_ok ? *reinterpret_cast<const uint32_t*>(zp) : 0u;
-      const uint32_t z1 = col_full ? *reinterpret_cast<const uint32_t*>(zp + 4) : 0u;
-      unpack8(z0, zh[0]);
-      unpack8(z1, zh[1]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        sh[0][j] = as_h2(s0[j]);
-        sh[1][j] = as_h2(s1[j]);
+      d.w[r] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw, w_off + (uint32_t)r * half_n, kw, NT));
+      if (TAIL) {
+        const uint32_t t = __builtin_amdgcn_raw_buffer_load_b32(rw, w_tail + (uint32_t)r * half_n, kw, NT);
+        d.w[r] = col_full ? d.w[r] : u32x2{t, 0u};
       }
     }
+    d.a = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off, live ? (uint32_t)(u * DEC_UNIT) * 2u : OOB, 0);
+  };
+  auto compute_unit = [&](const DecUnit& d) {
+    f16x2 zh[2][4], sh[2][4];
+    unpack8x(d.z0, zh[0]);
+    unpack8x(d.z1, zh[1]);
+    scales_x(d.s0, sh[0]);
+    scales_x(d.s1, sh[1]);
     const h8 af = __builtin_bit_cast(h8, d.a);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -654,19 +691,19 @@ __global__ void __launch_bounds__(DEC_THREADS)
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
         f16x2 hv[4];
-        unpack8(d.w[r][h], hv);
+        unpack8x(d.w[r][h], hv);
 #pragma unroll
         for (int j = 0; j < 4; ++j) dq[r][j] = as_u32((hv[j] - zh[h][j]) * sh[h][j]);
       }
+      // column cc (0..7) of the dword is pair (cc & 1) * 2 + (cc >> 2), half (cc >> 1) & 1
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const uint32_t sel = e ? 0x07060302u : 0x05040100u;
+      for (int cc = 0; cc < 8; ++cc) {
+          const int pj = (cc & 1) * 2 + (cc >> 2);
+          const uint32_t sel = ((cc >> 1) & 1) ? 0x07060302u : 0x05040100u;
           u32x4 col;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) col[q] = perm(dq[2 * q + 1][j], dq[2 * q][j], sel);
-          const int f = h * 8 + 2 * j + e;
+          for (int q = 0; q < 4; ++q) col[q] = perm(dq[2 * q + 1][pj], dq[2 * q][pj], sel);
+          const int f = h * 8 + cc;
           acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, __builtin_bit_cast(h8, col), acc[f], 0, 0, 0);
         }
     }
@@ -674,15 +711,12 @@ __global__ void __launch_bounds__(DEC_THREADS)
 
   DecUnit buf[DEC_DEPTH];
 #pragma unroll
-  for (int p = 0; p < DEC_DEPTH; ++p)
-    if (w_begin + p < w_end) load_unit(buf[p], w_begin + p);
+  for (int p = 0; p < DEC_DEPTH; ++p) load_unit(buf[p], w_begin + p);
   for (int u = w_begin; u < w_end; u += DEC_DEPTH) {
 #pragma unroll
     for (int p = 0; p < DEC_DEPTH; ++p) {
-      if (u + p < w_end) {
-        compute_unit(buf[p], u + p);
-        if (u + p + DEC_DEPTH < w_end) load_unit(buf[p], u + p + DEC_DEPTH);
-      }
+      compute_unit(buf[p]);  // a unit past the range holds zeros and adds nothing
+      load_unit(buf[p], u + p + DEC_DEPTH);
     }
   }
 
@@ -832,9 +866,14 @@ extern "C" tb_status tb_w4a16_gemm(const uint16_t* A, const uint8_t* W, const ui
     int* counters = reinterpret_cast<int*>(workspace);
     float* partials =
         need > 0 ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + DEC_COUNTER_BYTES) : nullptr;
-    hipLaunchKernelGGL(w4a16_decode, dim3((unsigned)(slabs * splits)), dim3(DEC_THREADS), 0, stream,
-                       reinterpret_cast<const _Float16*>(A), W, reinterpret_cast<const _Float16*>(scales), zeros,
-                       reinterpret_cast<_Float16*>(Y), partials, counters, (int)M, (int)N, (int)K, (int)group, splits);
+    if (N % 16 == 0)
+      hipLaunchKernelGGL(w4a16_decode<false>, dim3((unsigned)(slabs * splits)), dim3(DEC_THREADS), 0, stream,
+                         reinterpret_cast<const _Float16*>(A), W, reinterpret_cast<const _Float16*>(scales), zeros,
+                         reinterpret_cast<_Float16*>(Y), partials, counters, (int)M, (int)N, (int)K, (int)group, splits);
+    else
+      hipLaunchKernelGGL(w4a16_decode<true>, dim3((unsigned)(slabs * splits)), dim3(DEC_THREADS), 0, stream,
+                         reinterpret_cast<const _Float16*>(A), W, reinterpret_cast<const _Float16*>(scales), zeros,
+                         reinterpret_cast<_Float16*>(Y), partials, counters, (int)M, (int)N, (int)K, (int)group, splits);
     return tb::launch_status("tb_w4a16_gemm(decode)");
   }
   static bool attr_set = false;
