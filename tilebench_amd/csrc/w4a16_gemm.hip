@@ -270,27 +270,26 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
   };
   auto dequant_store = [&](const WRegs4& r, _Float16* st) {
     f16x2 zh[4], sh[4];
-    unpack8(r.z, zh);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) sh[j] = as_h2(r.s[j]);
+    unpack8x(r.z, zh);
+    scales_x(r.s, sh);
     uint32_t d[4][4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       f16x2 h[4];
-      unpack8(r.w[q], h);
+      unpack8x(r.w[q], h);
 #pragma unroll
       for (int j = 0; j < 4; ++j) d[q][j] = as_u32((h[j] - zh[j]) * sh[j]);
     }
+    // column cc of the 8 is pair (cc & 1) * 2 + (cc >> 2), half (cc >> 1) & 1
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const uint32_t sel = e ? 0x07060302u : 0x05040100u;
-        u32x2v col;
-        col[0] = perm(d[1][j], d[0][j], sel);
-        col[1] = perm(d[3][j], d[2][j], sel);
-        *reinterpret_cast<u32x2v*>(st + b_st[2 * j + e]) = col;
-      }
+    for (int cc = 0; cc < 8; ++cc) {
+      const int pj = (cc & 1) * 2 + (cc >> 2);
+      const uint32_t sel = ((cc >> 1) & 1) ? 0x07060302u : 0x05040100u;
+      u32x2v col;
+      col[0] = perm(d[1][pj], d[0][pj], sel);
+      col[1] = perm(d[3][pj], d[2][pj], sel);
+      *reinterpret_cast<u32x2v*>(st + b_st[cc]) = col;
+    }
   };
 
   f32x16 acc[4][2];
