@@ -192,21 +192,31 @@ __global__ void __launch_bounds__(THREADS, 1)
   uint16_t* ct = reinterpret_cast<uint16_t*>(lds);
   const int rbase = wm * 128 + (lane >> 5) * 4;
   const int cbase = wn * 64 + (lane & 31);
+  // Scales by buffer loads with out-of-range offsets past M or N (zeros): no
+  // branch around a load, so the 66 loads of a lane are in flight together
+  // instead of one round trip each.
+  const buf_rsrc_t rsa = buf_rsrc(sa, (uint32_t)M * 4u), rsw = buf_rsrc(sw, (uint32_t)N * 4u);
   float swv[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int n = tile.n0 + cbase + j * 32;
-    swv[j] = n < N ? sw[n] : 0.f;
+    swv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsw, n < N ? (uint32_t)n * 4u : OOB, 0, 0));
   }
+  float sav[4][16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int m = tile.m0 + rbase + i * 32 + (e >> 2) * 8 + (e & 3);
+      sav[i][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsa, m < M ? (uint32_t)m * 4u : OOB, 0, 0));
+    }
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int row = rbase + i * 32 + (e >> 2) * 8 + (e & 3);
-      const int m = tile.m0 + row;
-      const float sav = m < M ? sa[m] : 0.f;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) ct[row * C_STRIDE + cbase + j * 32] = bf16_rne(acc[i][j][e] * sav * swv[j]);
+      for (int j = 0; j < 2; ++j) ct[row * C_STRIDE + cbase + j * 32] = bf16_rne(acc[i][j][e] * sav[i][e] * swv[j]);
     }
   __syncthreads();
   const int rows = min(BM, M - tile.m0);

@@ -94,20 +94,24 @@ __global__ void __launch_bounds__(256) fp8_quant_rows(const u32x4* __restrict__ 
   const int64_t chunks = K >> 3;  // 8 halfs per 16-byte chunk
   const u32x4* src = A + row * chunks;
 
+  // Every chunk is a buffer load, chunks past the row end reading zeros (which
+  // leave the maximum unchanged): no branch around a load, so all of a
+  // thread's loads are in flight together.
+  const buf_rsrc_t rs = buf_rsrc(src, (uint32_t)(chunks * 16));
   u32x4 x[ITEMS];
-  uint32_t m = 0;  // packed pair of u16 magnitudes
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
     const int64_t ch = threadIdx.x + (int64_t)i * 256;
-    if (ch < chunks) {
-      x[i] = ld_nt(src + ch);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t a = x[i][j] & 0x7FFF7FFFu;
-        m = max(m & 0xFFFFu, a & 0xFFFFu) | (max(m >> 16, a >> 16) << 16);
-      }
-    }
+    x[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, ch < chunks ? (uint32_t)(ch * 16) : BUF_OOB, 0, 2 /* nt */);
   }
+  uint32_t m = 0;  // packed pair of u16 magnitudes
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t a = x[i][j] & 0x7FFF7FFFu;
+      m = max(m & 0xFFFFu, a & 0xFFFFu) | (max(m >> 16, a >> 16) << 16);
+    }
   m = max(m & 0xFFFFu, m >> 16);
   m = wave_max_u32(m);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;

@@ -257,12 +257,40 @@ __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64, 1)
   // Epilogue straight from registers: accumulator elements 4g .. 4g+3 of
   // fragment (i, j) are row i*32 + lane%32, columns j*32 + g*8 + (lane/32)*4 + 0..3
   // of the wave tile (N % 8 == 0, so four columns are all in or all out).
+  // The fp8 scales are fetched before any branch, by buffer loads that read
+  // zeros past M or N, so they are all in flight together.
+  float sav[FI];
+  f32x4 swv[FJ][4];
+#pragma unroll
+  for (int i = 0; i < FI; ++i) sav[i] = 1.f;
+#pragma unroll
+  for (int j = 0; j < FJ; ++j)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) swv[j][g] = f32x4{1.f, 1.f, 1.f, 1.f};
+  if constexpr (KIND == KIND_FP8) {
+    if (sa) {
+      const buf_rsrc_t rsa = buf_rsrc(sa, (uint32_t)M * 4u);
+#pragma unroll
+      for (int i = 0; i < FI; ++i) {
+        const int m = m0 + a_row + i * 32;
+        sav[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsa, m < M ? (uint32_t)m * 4u : BUF_OOB, 0, 0));
+      }
+    }
+    if (sw) {
+      const buf_rsrc_t rsw = buf_rsrc(sw, (uint32_t)N * 4u);
+#pragma unroll
+      for (int j = 0; j < FJ; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = n0 + wn * WN + j * 32 + g * 8 + (lane >> 5) * 4;
+          swv[j][g] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsw, n < N ? (uint32_t)n * 4u : BUF_OOB, 0, 0));
+        }
+    }
+  }
 #pragma unroll
   for (int i = 0; i < FI; ++i) {
     const int m = m0 + a_row + i * 32;
     if (m >= M) continue;
-    float sav = 1.f;
-    if constexpr (KIND == KIND_FP8) sav = sa ? sa[m] : 1.f;
 #pragma unroll
     for (int j = 0; j < FJ; ++j)
 #pragma unroll
@@ -286,10 +314,7 @@ __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64, 1)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             float x = acc[i][j][4 * g + q];
-            if constexpr (KIND == KIND_FP8) {
-              const float swv = sw ? sw[n + q] : 1.f;
-              x = x * sav * swv;
-            }
+            if constexpr (KIND == KIND_FP8) x = x * sav[i] * swv[j][g][q];
             b[q] = bf16_bits(x);
           }
           if constexpr (OUT == OUT_BF16) {

@@ -61,6 +61,16 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
   return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
+// Raw buffer resource over `bytes` bytes at p: loads through it at offsets past
+// the end return zeros without touching memory, so a load can be issued for
+// every lane, with an out-of-range offset where there is nothing to read,
+// instead of sitting behind a per-lane branch.
+typedef __amdgpu_buffer_rsrc_t buf_rsrc_t;
+constexpr uint32_t BUF_OOB = 0x80000000u;
+__device__ __forceinline__ buf_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
+}
+
 __device__ __forceinline__ f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
 __device__ __forceinline__ uint32_t as_u32(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
 
