@@ -125,20 +125,37 @@ __global__ void __launch_bounds__(ALIGN_THREADS)
 
 // out[t, c .. c+7] = fp16(sum_j fp32(y[t * topk + j, c .. c+7])), slots with an
 // expert id outside [0, experts) skipped.  One 16-byte granule per thread.
+// All of a token's ids are loaded first, then all its rows (an unrouted slot
+// through an out-of-range offset, reading zeros without memory traffic, and
+// skipped in the sum so that results do not depend on it): one round trip
+// per thread instead of one per slot.
+template <int KMAX>
 __global__ void __launch_bounds__(256)
     moe_combine_kernel(const u32x4* __restrict__ y, const int* __restrict__ ids, u32x4* __restrict__ out,
                        int64_t tokens, int topk, int experts, int64_t g_per_row) {
   const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (g >= tokens * g_per_row) return;
   const int64_t tok = g / g_per_row, c = g - tok * g_per_row;
+  const buf_rsrc_t rid = buf_rsrc(ids + tok * topk, (uint32_t)topk * 4u);
+  int id[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j)
+    id[j] = (int)__builtin_amdgcn_raw_buffer_load_b32(rid, j < topk ? (uint32_t)j * 4u : BUF_OOB, 0, 0);
+  const buf_rsrc_t ry = buf_rsrc(y + tok * topk * g_per_row, (uint32_t)(topk * g_per_row * 16));
+  u32x4 v[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    const bool ok = j < topk && (unsigned)id[j] < (unsigned)experts;
+    v[j] = __builtin_amdgcn_raw_buffer_load_b128(ry, ok ? (uint32_t)((j * g_per_row + c) * 16) : BUF_OOB, 0,
+                                                 2 /* nt */);
+  }
   float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < topk; ++j) {
-    const int64_t p = tok * topk + j;
-    if ((unsigned)ids[p] >= (unsigned)experts) continue;
-    const u32x4 v = __builtin_nontemporal_load(y + p * g_per_row + c);
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    if (!(j < topk && (unsigned)id[j] < (unsigned)experts)) continue;  // slot order, unrouted slots skipped
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const f16x2 h = as_h2(v[q]);
+      const f16x2 h = as_h2(v[j][q]);
       s[2 * q] += (float)h[0];
       s[2 * q + 1] += (float)h[1];
     }
@@ -206,15 +223,22 @@ extern "C" tb_status tb_moe_combine(const uint16_t* y, const int32_t* topk_ids, 
   TB_CHECK_ARG(tokens > 0 && topk > 0 && experts > 0 && H > 0, "tb_moe_combine: sizes must be positive");
   TB_CHECK_ARG(H % 8 == 0, "tb_moe_combine: H must be a multiple of 8 (got %lld)", (long long)H);
   TB_CHECK_ARG(tokens * topk < (1ll << 31), "tb_moe_combine: tokens * topk must be < 2^31");
+  TB_CHECK_ARG(topk <= 32, "tb_moe_combine: topk must be at most 32 (got %lld)", (long long)topk);
+  TB_CHECK_ARG(topk * H * 2 < (1ll << 31), "tb_moe_combine: a token's topk rows must be < 2 GiB");
   TB_CHECK_ALIGN(y, 16, "y");
   TB_CHECK_ALIGN(out, 16, "out");
   TB_CHECK_ALIGN(topk_ids, 4, "topk_ids");
   const int64_t g_per_row = H / 8, granules = tokens * g_per_row;
   const int64_t blocks = (granules + 255) / 256;
   TB_CHECK_ARG(blocks < (1ll << 31), "tb_moe_combine: problem too large");
-  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
-                     reinterpret_cast<const tb::u32x4*>(y), topk_ids, reinterpret_cast<tb::u32x4*>(out), tokens, (int)topk,
-                     (int)experts, g_per_row);
+  auto* yv = reinterpret_cast<const tb::u32x4*>(y);
+  auto* ov = reinterpret_cast<tb::u32x4*>(out);
+  if (topk <= 8)
+    hipLaunchKernelGGL(moe_combine_kernel<8>, dim3((unsigned)blocks), dim3(256), 0, stream, yv, topk_ids, ov, tokens,
+                       (int)topk, (int)experts, g_per_row);
+  else
+    hipLaunchKernelGGL(moe_combine_kernel<32>, dim3((unsigned)blocks), dim3(256), 0, stream, yv, topk_ids, ov, tokens,
+                       (int)topk, (int)experts, g_per_row);
   return tb::launch_status("tb_moe_combine");
 }
 
