@@ -162,7 +162,7 @@ def _w_w4a16(M):
                     unit="TFLOP/s" if big else "GB/s", dtype="fp16 x int4 -> fp16 (fp32 acc)",
                     bound="mfma" if big else "hbm", peak_key="fp16", bytes=nbytes, flops=flops, out_bytes=2 * M * N,
                     inputs=inputs, step=lambda x: impl_hip.run(*x),
-                    kernel="tb::w4a16::w4a16_prefill" if big else "tb::w4a16::w4a16_decode", cpu_sample=cpu_sample)
+                    kernel="tb::w4a16::w4a16_prefill" if big else "tb::w4a16::w4a16_decode<false>", cpu_sample=cpu_sample)
     return make
 
 

@@ -143,6 +143,7 @@ def test_probe_needs_a_gpu(monkeypatch, capsys):
     ("_ZN2tb5w4a1613w4a16_prefillEPKDF16_PKhS2_S4_PDF16_iiiiii", "tb::w4a16::w4a16_prefill"),
     ("_ZN2tb13gating_kernelILi0ELi16ELi16ELi2EEEvPKvPvPilii", "tb::gating_kernel<0, 16, 16, 2>"),
     ("_ZN2tb11copy_kernelEPKDv4_jPS0_l", "tb::copy_kernel"),
+    ("_ZN2tb5w4a1612w4a16_decodeILb0EEEvPKDF16_PKhS3_S5_PDF16_PfPiiiiii", "tb::w4a16::w4a16_decode<false>"),
 ])
 def test_mangled_symbols_as_the_profilers_report_them(mangled, stem):
     """torch.profiler names a HIP kernel by its mangled symbol, rocprofv3 by

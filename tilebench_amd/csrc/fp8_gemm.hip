@@ -246,15 +246,8 @@ extern "C" tb_status tb_fp8_scaled_gemm(const uint8_t* Aq, const uint8_t* WqT, c
   TB_CHECK_ALIGN(Aq, 16, "Aq");
   TB_CHECK_ALIGN(WqT, 16, "WqT");
   TB_CHECK_ALIGN(Y, 16, "Y");
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&fp8_gemm_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BYTES) != hipSuccess) {
-      tb::set_error("tb_fp8_scaled_gemm: cannot reserve %zu bytes of LDS", LDS_BYTES);
-      return TB_E_HIP;
-    }
-    attr_set = true;
-  }
+  if (tb_status st = tb::reserve_lds(reinterpret_cast<const void*>(&fp8_gemm_kernel), LDS_BYTES, "tb_fp8_scaled_gemm"))
+    return st;
   const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
   hipLaunchKernelGGL(fp8_gemm_kernel, dim3(tiles_m * tiles_n), dim3(THREADS), LDS_BYTES, stream, Aq, WqT, sa, sw, Y,
                      (int)M, (int)N, (int)K, tiles_m, tiles_n);

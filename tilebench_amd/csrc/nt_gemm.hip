@@ -486,15 +486,7 @@ tb_status launch_nt(const uint8_t* A, const uint8_t* BT, void* Y, const float* s
                     int64_t N, int64_t Kb, hipStream_t stream, const char* what) {
   auto kern = &nt_gemm<KIND, OUT, BM, BN, WM, WN>;
   constexpr size_t lds = (size_t)2 * (BM + BN) * BK;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)lds) != hipSuccess) {
-      set_error("%s: cannot reserve %zu bytes of LDS", what, lds);
-      return TB_E_HIP;
-    }
-    attr_set = true;
-  }
+  if (tb_status st = reserve_lds(reinterpret_cast<const void*>(kern), lds, what)) return st;
   const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
   constexpr int threads = (BM / WM) * (BN / WN) * 64;
   hipLaunchKernelGGL(kern, dim3(tiles_m * tiles_n), dim3(threads), lds, stream, A, BT, Y, sa, sw, (int)M, (int)N,

@@ -36,6 +36,11 @@ inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintp
     }                                                                                   \
   } while (0)
 
+// Allow `kernel` up to `bytes` of dynamic LDS on the current device.  The
+// attribute is set once per (kernel, device) pair (a process may drive several
+// GPUs); thread-safe.
+tb_status reserve_lds(const void* kernel, size_t bytes, const char* what);
+
 // Report the status of the launch that was just enqueued.
 inline tb_status launch_status(const char* what) {
   hipError_t e = hipGetLastError();

@@ -4,6 +4,8 @@
 
 #include <string.h>
 
+#include <mutex>
+
 namespace tb {
 
 static thread_local char g_last_error[512] = {0};
@@ -13,6 +15,30 @@ void set_error(const char* fmt, ...) {
   va_start(ap, fmt);
   vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
   va_end(ap);
+}
+
+tb_status reserve_lds(const void* kernel, size_t bytes, const char* what) {
+  struct Entry {
+    const void* kernel;
+    int device;
+  };
+  static std::mutex mu;
+  static Entry done[256];
+  static int n_done = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    set_error("%s: no current device", what);
+    return TB_E_HIP;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < n_done; ++i)
+    if (done[i].kernel == kernel && done[i].device == dev) return TB_OK;
+  if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) != hipSuccess) {
+    set_error("%s: cannot reserve %zu bytes of LDS", what, bytes);
+    return TB_E_HIP;
+  }
+  if (n_done < 256) done[n_done++] = Entry{kernel, dev};  // past 256 pairs the attribute is simply set again
+  return TB_OK;
 }
 
 // Streaming kernels are written one 16-byte granule per thread over a grid

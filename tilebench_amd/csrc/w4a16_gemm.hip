@@ -875,15 +875,7 @@ extern "C" tb_status tb_w4a16_gemm(const uint16_t* A, const uint8_t* W, const ui
                          reinterpret_cast<_Float16*>(Y), partials, counters, (int)M, (int)N, (int)K, (int)group, splits);
     return tb::launch_status("tb_w4a16_gemm(decode)");
   }
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a16_prefill), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)LDS4_BYTES) != hipSuccess) {
-      tb::set_error("tb_w4a16_gemm: cannot reserve %zu bytes of LDS", LDS4_BYTES);
-      return TB_E_HIP;
-    }
-    attr_set = true;
-  }
+  if (tb_status st = tb::reserve_lds(reinterpret_cast<const void*>(&w4a16_prefill), LDS4_BYTES, "tb_w4a16_gemm")) return st;
   const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
   hipLaunchKernelGGL(w4a16_prefill, dim3(tiles_m * tiles_n), dim3(T4), LDS4_BYTES, stream,
                      reinterpret_cast<const _Float16*>(A), W, reinterpret_cast<const _Float16*>(scales), zeros,
@@ -909,15 +901,7 @@ extern "C" tb_status tb_moe_w4a16_grouped_gemm(const uint16_t* A, const uint8_t*
   TB_CHECK_ALIGN(scales, 16, "scales");
   TB_CHECK_ALIGN(zeros, 4, "zeros");
   TB_CHECK_ALIGN(Y, 16, "Y");
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a16_grouped), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)LDS4_BYTES) != hipSuccess) {
-      tb::set_error("tb_moe_w4a16_grouped_gemm: cannot reserve %zu bytes of LDS", LDS4_BYTES);
-      return TB_E_HIP;
-    }
-    attr_set = true;
-  }
+  if (tb_status st = tb::reserve_lds(reinterpret_cast<const void*>(&w4a16_grouped), LDS4_BYTES, "tb_moe_w4a16_grouped_gemm")) return st;
   const int64_t tiles_n = (N + BN - 1) / BN;
   const int64_t tile_rows = (R + BM - 1) / BM + experts;  // upper bound on sum_e ceil(rows_e / 256)
   const int64_t blocks = tile_rows * tiles_n;
@@ -928,21 +912,6 @@ extern "C" tb_status tb_moe_w4a16_grouped_gemm(const uint16_t* A, const uint8_t*
   return tb::launch_status("tb_moe_w4a16_grouped_gemm");
 }
 
-namespace {
-// Reserve the tile routine's 160 KiB of dynamic LDS for a kernel, once.
-template <typename F>
-tb_status reserve_lds(F* kernel, bool& done, const char* what) {
-  if (!done) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)tb::w4a16::LDS4_BYTES) != hipSuccess) {
-      tb::set_error("%s: cannot reserve %zu bytes of LDS", what, tb::w4a16::LDS4_BYTES);
-      return TB_E_HIP;
-    }
-    done = true;
-  }
-  return TB_OK;
-}
-}  // namespace
 
 extern "C" tb_status tb_moe_w4a16_gate_up(const uint16_t* X, const int32_t* sorted_ids, const int32_t* offsets,
                                           const uint8_t* W13, const uint16_t* S13, const uint8_t* Z13, uint16_t* act,
@@ -966,8 +935,7 @@ extern "C" tb_status tb_moe_w4a16_gate_up(const uint16_t* X, const int32_t* sort
   TB_CHECK_ALIGN(S13, 16, "S13");
   TB_CHECK_ALIGN(Z13, 4, "Z13");
   TB_CHECK_ALIGN(act, 16, "act");
-  static bool lds_ok = false;
-  if (tb_status st = reserve_lds(&moe_gate_up, lds_ok, fn)) return st;
+  if (tb_status st = tb::reserve_lds(reinterpret_cast<const void*>(&moe_gate_up), LDS4_BYTES, fn)) return st;
   const int64_t tiles_n = (I + BN / 2 - 1) / (BN / 2);
   const int64_t tile_rows = (pairs + BM - 1) / BM + experts;
   const int64_t blocks = tile_rows * tiles_n;
@@ -999,8 +967,7 @@ extern "C" tb_status tb_moe_w4a16_down(const uint16_t* act, const int32_t* sorte
   TB_CHECK_ALIGN(S2, 16, "S2");
   TB_CHECK_ALIGN(Z2, 4, "Z2");
   TB_CHECK_ALIGN(Y, 16, "Y");
-  static bool lds_ok = false;
-  if (tb_status st = reserve_lds(&moe_down, lds_ok, fn)) return st;
+  if (tb_status st = tb::reserve_lds(reinterpret_cast<const void*>(&moe_down), LDS4_BYTES, fn)) return st;
   const int64_t tiles_n = (H + BN - 1) / BN;
   const int64_t tile_rows = (pairs + BM - 1) / BM + experts;
   const int64_t blocks = tile_rows * tiles_n;

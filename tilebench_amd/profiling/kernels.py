@@ -132,8 +132,8 @@ def _split_scope(stem: str) -> list[str]:
 def mangled_prefix_regex(stem: str):
     """The Itanium-mangled prefix of a kernel stem as a regex, e.g.
     `tb::ntg::nt_gemm<3, 4>` -> `_ZN2tb3ntg7nt_gemmIL[a-z]+3EL[a-z]+4EEE`
-    (integer template arguments of any integer type); None when a template
-    argument is not an integer literal."""
+    (integer template arguments of any integer type, `false` / `true` as
+    `Lb0E` / `Lb1E`); None when a template argument is anything else."""
     out = "_ZN"
     for comp in _split_scope(stem):
         name, _, targs = comp.partition("<")
@@ -142,9 +142,15 @@ def mangled_prefix_regex(stem: str):
         out += f"{len(name)}{name}"
         if targs:
             args = [a.strip() for a in targs.rstrip(">").split(",")]
-            if not all(re.fullmatch(r"-?[0-9]+", a) for a in args):
-                return None
-            out += "I" + "".join("L[a-z]+" + ("n" + a[1:] if a.startswith("-") else a) + "E" for a in args) + "E"
+            parts = []
+            for a in args:
+                if a in ("false", "true"):
+                    parts.append("Lb" + ("1" if a == "true" else "0") + "E")
+                elif re.fullmatch(r"-?[0-9]+", a):
+                    parts.append("L[a-z]+" + ("n" + a[1:] if a.startswith("-") else a) + "E")
+                else:
+                    return None
+            out += "I" + "".join(parts) + "E"
     return out + "E"
 
 
