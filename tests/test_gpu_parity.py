@@ -92,6 +92,80 @@ def test_gating_ties_nan_signed_zero(gpu):
     np.testing.assert_allclose(w.cpu().numpy(), rw, atol=1e-5, rtol=1e-5, equal_nan=True)
 
 
+def _filter_rows(E):
+    """Rows that steer the filter kernel (E = 16·V, 16 lanes per row, lane q
+    owning elements c·64 + 4q + i in fp32) through both of its paths: the
+    threshold T is the k-th largest lane maximum and the row's candidates are
+    the elements >= T.  Results are checked against the oracle either way."""
+    rng = np.random.default_rng(E)
+    rows = []
+    base = lambda: rng.uniform(-5, -1, E).astype(np.float32)
+    r = base(); r[np.arange(16) * 4] = 1.0                 # 16 tied candidates: filter path
+    rows.append(r)
+    r = base(); r[np.arange(16) * 4] = 1.0; r[1] = 1.0     # 17 candidates: exact path for its wavefront
+    rows.append(r)
+    r = base(); r[np.arange(16) * 4] = 0.0; r[8] = -0.0; r[2] = -0.0   # signed zeros at the threshold
+    rows.append(r)
+    r = base(); r[np.arange(8) * 8] = 2.0; r[np.arange(8) * 8 + 2] = 2.0  # ties inside lanes
+    rows.append(r)
+    r = rng.standard_normal(E).astype(np.float32); r[E // 3] = np.inf
+    rows.append(r)
+    r = rng.standard_normal(E).astype(np.float32); r[E - 1] = np.nan
+    rows.append(r)
+    r = rng.standard_normal(E).astype(np.float32); r[5] = -np.inf
+    rows.append(r)
+    r = np.full(E, 3.0, np.float32)                          # every element tied
+    rows.append(r)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("E", [64, 128, 256])
+@pytest.mark.parametrize("k", [1, 2, 3, 7, 8])
+def test_gating_filter_paths(gpu, E, k):
+    """The filter kernel's shapes (E in {64, 128, 256}, k <= 8): random rows
+    (filter path) mixed with rows that force the exact path for their
+    wavefront (more than 16 candidates, inf, NaN), ties and signed zeros at
+    the threshold, and a ragged row count."""
+    from tilebench_amd.benchmarks.operators.moe_topk_gating import impl_hip
+
+    _say("gating filter paths", E, k)
+    rng = np.random.default_rng(100 * E + k)
+    x = rng.standard_normal((1001, E)).astype(np.float32)
+    special = _filter_rows(E)
+    x[17:17 + len(special)] = special            # in the wavefronts of rows 16..19, 20..23, 24..27
+    x[600:600 + len(special)] = special[::-1]
+    w, i = impl_hip.run(torch.from_numpy(x).to(gpu), x.shape[0], E, k)
+    torch.cuda.synchronize()
+    rw, ri = oracle.moe_topk_gating(x, k)
+    np.testing.assert_array_equal(i.cpu().numpy(), ri)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, atol=1e-5, rtol=1e-5, equal_nan=True)
+
+
+@pytest.mark.parametrize("E", [64, 256])
+@pytest.mark.parametrize("dt", ["fp16", "bf16"])
+def test_gating_filter_half_dtypes(gpu, E, dt):
+    """fp16 / bf16 logits at the BASELINE shapes (k = 8): indices bit-exact;
+    weights within one unit in the last place of the half type (the fp32
+    softmax matches the oracle to ~1e-7, so a rounding to half may land one
+    step away)."""
+    from tilebench_amd.benchmarks.operators.moe_topk_gating import impl_hip
+
+    _say("gating filter", E, dt)
+    tdt = torch.float16 if dt == "fp16" else torch.bfloat16
+    logits, M, E, k = T.generate_moe_topk_gating_inputs(4099, E, 8, dtype=tdt, seed=E, device="cpu")
+    logits[40:48] = torch.from_numpy(_filter_rows(E)).to(tdt)
+    w, i = impl_hip.run(logits.to(gpu), M, E, k)
+    torch.cuda.synchronize()
+    bits = logits.view(torch.int16).numpy().view(np.uint16) if dt == "bf16" else logits.numpy()
+    rw, ri = oracle.moe_topk_gating(bits, k, dtype=dt)
+    np.testing.assert_array_equal(i.cpu().numpy(), ri)
+    got = _u16(w).astype(np.int32)
+    want = np.asarray(rw).view(np.uint16).astype(np.int32)
+    nan = np.isnan(w.float().cpu().numpy())
+    assert np.array_equal(nan, np.isnan(oracle.bf16_bits_to_f32(rw) if dt == "bf16" else rw.astype(np.float32)))
+    assert np.abs(got - want)[~nan].max() <= 1
+
+
 @pytest.mark.parametrize("dt", ["fp16", "bf16"])
 def test_gating_half_dtypes(gpu, dt):
     from tilebench_amd.benchmarks.operators.moe_topk_gating import impl_hip

@@ -1,28 +1,52 @@
 // MoE router gating: per row, top-k logits (descending, equal logits -> lowest
 // expert index first) and the softmax over those k logits in fp32.
 //
-// Layout: a row is owned by LPR consecutive lanes (a power of two), lane q
-// holding elements q*V .. q*V+V-1 (V = 16) in registers, loaded with 16-byte
-// loads: the lanes of a row read it with one contiguous sweep and consecutive
-// rows follow, so the logits stream straight from HBM into registers, with no
-// LDS staging and no barrier.
+// Two kernels share the exact selection code below.
 //
-// Each logit becomes an order-preserving uint32 key, and each (key, index)
-// pair one double holding the integer 2^52 + key*1024 + (1023 - index): the
-// double order is the selection order (larger key first, then lower index),
-// and no two elements of a row are equal, so a compare-exchange is one max
-// and one min.  Every lane sorts its V elements (a Batcher network, pruned by
-// the compiler to the entries that can be selected).  k rounds follow: the
-// LPR lanes take the maximum of their list heads with an xor-butterfly, which
-// leaves every lane of the row with the winner, and the lane that held it
-// pops its list.  Selection runs on the logits themselves, never on exp()
-// values, so rounding in exp cannot create or break ties.  Lane t % LPR
-// writes output t (weights and indices of a row land in one coalesced store).
+// filter_kernel (E = 16·V with V in {4, 8, 16} and 2 < k <= 8: the BASELINE
+// shapes).  A row is owned by 16 lanes; each lane loads V logits
+// with 16-byte loads (8-byte when V·size < 16) laid out so that one load
+// instruction of the row's 16 lanes covers 256 contiguous bytes.  The row is
+// also staged in LDS as loaded.  Per lane:
+//   1. the lane maximum m_q (signed-int order of the float bits, two VALU ops
+//      per element for the key, max3/min3 folds);
+//   2. T = the k-th largest of the 16 lane maxima (a bitonic network across
+//      the row's lanes).  The k lanes with the largest maxima hold k distinct
+//      elements >= T, so the row's k-th largest element is >= T, and every
+//      element the top-k can select is >= T;
+//   3. the lane's candidates, elements >= T (float compare: -0 == +0), as a
+//      bit mask built with one compare and one add-with-carry per element;
+//   4. the row's candidates are compacted (prefix sum of the lane counts) into
+//      an LDS list of row indices; with at most 16 of them, lane i takes
+//      candidate i as the exact (key, 1023 - index) pair and a bitonic network
+//      over the 16 lanes sorts them: lane t ends with the t-th selection.
+// On random logits a row has about 10 candidates at k = 8; 2.6 % of the
+// wavefronts at E = 256 (0.2 % at E = 64) have a row with more than 16.  A
+// wavefront any of whose rows has more than 16, or holds inf or NaN, runs the
+// exact path below on the staged rows instead (same results, more work).
+//
+// exact path (every other shape, and the fallback).  A row is owned by LPR
+// consecutive lanes (a power of two), lane q holding elements q*V .. q*V+V-1
+// in registers.  Each logit becomes an order-preserving uint32 key, and each
+// (key, index) pair one double holding the integer 2^52 + key*1024 + (1023 -
+// index): the double order is the selection order (larger key first, then
+// lower index), and no two elements of a row are equal, so a compare-exchange
+// is one max and one min.  Every lane sorts its V elements (a Batcher network,
+// pruned by the compiler to the entries that can be selected).  k rounds
+// follow: the LPR lanes take the maximum of their list heads with an
+// xor-butterfly, which leaves every lane of the row with the winner, and the
+// lane that held it pops its list.  Selection runs on the logits themselves,
+// never on exp() values, so rounding in exp cannot create or break ties.
 //
 // Key map: k(x) = 0x80000000 + |x| bits for x >= 0 and 0x80000000 - |x| bits
 // for x < 0, so -0.0 and +0.0 meet at 0x80000000 (they compare equal), and
 // every NaN maps to 0xFFFFFFFF (a NaN ranks above +inf, as in torch.topk).
 // Real keys are >= k(-inf) = 0x00800000, so 0 marks an absent slot.
+//
+// The softmax denominator adds the k exponentials in numpy's order for a
+// float32 row sum (left to right below 8 terms; 8 strided partial sums joined
+// as a tree from 8 on, then the remainder), the order the CPU oracle's
+// `e.sum(axis=1, dtype=float32)` uses.
 #include "tb_common.h"
 
 #include <utility>
@@ -41,6 +65,13 @@ __device__ __forceinline__ float float_of_key(uint32_t u) {
   return __builtin_bit_cast(float, b);
 }
 
+// Signed-int order of float bits: for floats a < b, flip(a) < flip(b) as
+// int32, with -0.0 just below +0.0; NaN and inf land beyond +-inf's keys.  The
+// map is its own inverse.
+__device__ __forceinline__ int32_t flip_key(uint32_t b) {
+  return (int32_t)(b ^ ((uint32_t)((int32_t)b >> 31) & 0x7FFFFFFFu));
+}
+
 // Round-to-nearest-even fp32 -> bf16 (NaN stays a quiet NaN).
 __device__ __forceinline__ uint16_t bf16_rne(float f) {
   const uint32_t b = __builtin_bit_cast(uint32_t, f);
@@ -48,16 +79,26 @@ __device__ __forceinline__ uint16_t bf16_rne(float f) {
   return (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
 }
 
+// fp32 bits of element `j` of a logits word (fp32: the word; fp16/bf16: half
+// j & 1 of the word).
+template <int DT>
+__device__ __forceinline__ uint32_t f32_bits(uint32_t word, int half) {
+  if constexpr (DT == 0) {
+    return word;
+  } else {
+    const uint32_t h = half ? word >> 16 : word & 0xFFFFu;
+    if constexpr (DT == 1) return __builtin_bit_cast(uint32_t, (float)__builtin_bit_cast(_Float16, (uint16_t)h));
+    return h << 16;
+  }
+}
+
 template <int DT>
 __device__ __forceinline__ uint32_t load_key(const void* base, int64_t i) {
   if constexpr (DT == 0) {
     return key_of_bits(reinterpret_cast<const uint32_t*>(base)[i]);
-  } else if constexpr (DT == 1) {
-    const uint16_t h = reinterpret_cast<const uint16_t*>(base)[i];
-    return key_of_bits(__builtin_bit_cast(uint32_t, (float)__builtin_bit_cast(_Float16, h)));
   } else {
     const uint16_t h = reinterpret_cast<const uint16_t*>(base)[i];
-    return key_of_bits((uint32_t)h << 16);
+    return key_of_bits(f32_bits<DT>(h, 0));
   }
 }
 
@@ -70,6 +111,38 @@ __device__ __forceinline__ void store_weight(void* base, int64_t i, float w) {
   } else {
     reinterpret_cast<uint16_t*>(base)[i] = bf16_rne(w);
   }
+}
+
+// numpy's float32 sum of e[0 .. n-1] (n <= N): a left-to-right loop below 8
+// terms; from 8 on, eight partial sums r[j] = e[j] + e[j+8] + ... over the
+// whole blocks of 8, joined as ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)), then the
+// remaining n % 8 terms left to right.
+template <int N>
+__device__ __forceinline__ float np_sum(const float (&e)[N], int n) {
+  float s = e[0];
+  if (N < 8 || n < 8) {
+#pragma unroll
+    for (int t = 1; t < (N < 8 ? N : 8); ++t)
+      if (t < n) s += e[t];
+    return s;
+  }
+  if constexpr (N >= 8) {
+    float r[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = e[j];
+    const int whole = n - n % 8;
+#pragma unroll
+    for (int i = 8; i + 8 <= N; i += 8)
+      if (i < whole) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] += e[i + j];
+      }
+    s = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+#pragma unroll
+    for (int t = 8; t < N; ++t)
+      if (t >= whole && t < n) s += e[t];
+  }
+  return s;
 }
 
 constexpr int kBlock = 256;
@@ -163,45 +236,12 @@ __device__ __forceinline__ double xchg_elem(double v, int step) {
   return __builtin_bit_cast(double, b);
 }
 
-template <int DT, int V, int LPR, int KMAX>
-__global__ void __launch_bounds__(kBlock) gating_kernel(const void* __restrict__ logits, void* __restrict__ weights,
-                                                        int32_t* __restrict__ indices, int64_t M, int E, int k) {
-  constexpr int ROWS = kBlock / LPR;
-  constexpr int ESZ = DT == 0 ? 4 : 2;
+// Exact selection: lane q of the row's LPR lanes holds the keys of elements
+// q*V .. q*V+V-1 in u; every lane of the row returns the row's KMAX largest
+// elements (packed as above), largest first.
+template <int V, int LPR, int KMAX>
+__device__ __forceinline__ void exact_select(const uint32_t (&u)[V], int q, double (&sel)[KMAX]) {
   constexpr int L = KMAX < V ? KMAX : V;  // list entries a lane can ever contribute
-  const int64_t r = (int64_t)blockIdx.x * ROWS + threadIdx.x / LPR;
-  const int q = threadIdx.x % LPR;
-  if (r >= M) return;  // whole LPR groups leave together
-
-  // Keys of this lane's elements: one 16-byte load when the chunk lies inside
-  // the row and rows are 16-byte multiples (so the load is aligned), else
-  // element loads (never past the end of the row).
-  uint32_t u[V];
-  {
-    const int c0 = q * V;
-    const char* rowp = reinterpret_cast<const char*>(logits) + (r * E + c0) * ESZ;
-    const bool aligned16 = ((E * ESZ) & 15) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0;
-    if (c0 + V <= E && aligned16) {
-      constexpr int NV = V * ESZ / 16;
-      u32x4 x[NV];
-#pragma unroll
-      for (int b = 0; b < NV; ++b) x[b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rowp) + b);
-#pragma unroll
-      for (int j = 0; j < V; ++j) {
-        uint32_t fb;
-        if constexpr (DT == 0) {
-          fb = x[j / 4][j % 4];
-        } else {
-          const uint32_t h = (x[j / 8][(j % 8) >> 1] >> (16 * (j & 1))) & 0xFFFFu;
-          fb = DT == 1 ? __builtin_bit_cast(uint32_t, (float)__builtin_bit_cast(_Float16, (uint16_t)h)) : (h << 16);
-        }
-        u[j] = key_of_bits(fb);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < V; ++j) u[j] = c0 + j < E ? load_key<DT>(logits, r * E + c0 + j) : 0u;
-    }
-  }
 
   // The lane's L largest elements, largest first.  Absent elements (past E)
   // have key 0 and rank below every real one; k <= E keeps them unselected.
@@ -230,9 +270,7 @@ __global__ void __launch_bounds__(kBlock) gating_kernel(const void* __restrict__
   // KMAX rounds (straight-line code; those past k are not used): the row's
   // largest remaining element is the maximum of the LPR list heads
   // (xor-butterfly: every lane of the row ends with it), and the lane whose
-  // head it is (values are unique in a row) pops its list.  Round t reads
-  // only the first KMAX - t entries, so the shifts shrink round by round.
-  double sel[KMAX];
+  // head it is (values are unique in a row) pops its list.
 #pragma unroll
   for (int t = 0; t < KMAX; ++t) {
     double best = s[0];
@@ -245,21 +283,18 @@ __global__ void __launch_bounds__(kBlock) gating_kernel(const void* __restrict__
     next[L - 1] = 0.0;
     s = s[0] == best ? next : s;
   }
+}
 
-  // softmax over the k selected logits in fp32, summed in selection order
+// Softmax over the row's k selections (every lane of the row holds all of
+// them) and the stores: lane q writes outputs q, q + LPR, ...
+template <int DT, int LPR, int KMAX>
+__device__ __forceinline__ void write_selected(const double (&sel)[KMAX], int64_t r, int q, int k,
+                                               void* __restrict__ weights, int32_t* __restrict__ indices) {
   const float v0 = float_of_key(elem_key(sel[0]));
   float e[KMAX];
-  float sum = 0.f;
 #pragma unroll
-  for (int t = 0; t < KMAX; ++t) {
-    e[t] = 0.f;
-    if (t < k) {
-      e[t] = expf(float_of_key(elem_key(sel[t])) - v0);
-      sum += e[t];
-    }
-  }
-  // Lane q writes outputs q, q + LPR, ...: pick each one's values by selects
-  // and divide once per output written.
+  for (int t = 0; t < KMAX; ++t) e[t] = t < k ? expf(float_of_key(elem_key(sel[t])) - v0) : 0.f;
+  const float sum = np_sum<KMAX>(e, k);
   const int64_t out0 = r * k;
   constexpr int SLOTS = (KMAX + LPR - 1) / LPR;
 #pragma unroll
@@ -281,6 +316,237 @@ __global__ void __launch_bounds__(kBlock) gating_kernel(const void* __restrict__
 }
 
 template <int DT, int V, int LPR, int KMAX>
+__global__ void __launch_bounds__(kBlock) gating_kernel(const void* __restrict__ logits, void* __restrict__ weights,
+                                                        int32_t* __restrict__ indices, int64_t M, int E, int k) {
+  constexpr int ROWS = kBlock / LPR;
+  constexpr int ESZ = DT == 0 ? 4 : 2;
+  const int64_t r = (int64_t)blockIdx.x * ROWS + threadIdx.x / LPR;
+  const int q = threadIdx.x % LPR;
+  if (r >= M) return;  // whole LPR groups leave together
+
+  // Keys of this lane's elements: one 16-byte load when the chunk lies inside
+  // the row and rows are 16-byte multiples (so the load is aligned), else
+  // element loads (never past the end of the row).
+  uint32_t u[V];
+  {
+    const int c0 = q * V;
+    const char* rowp = reinterpret_cast<const char*>(logits) + (r * E + c0) * ESZ;
+    const bool aligned16 = ((E * ESZ) & 15) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0;
+    if (c0 + V <= E && aligned16) {
+      constexpr int NV = V * ESZ / 16;
+      u32x4 x[NV];
+#pragma unroll
+      for (int b = 0; b < NV; ++b) x[b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rowp) + b);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const int w = j * ESZ / 4;
+        u[j] = key_of_bits(f32_bits<DT>(x[w / 4][w % 4], j & 1));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) u[j] = c0 + j < E ? load_key<DT>(logits, r * E + c0 + j) : 0u;
+    }
+  }
+  double sel[KMAX];
+  exact_select<V, LPR, KMAX>(u, q, sel);
+  write_selected<DT, LPR, KMAX>(sel, r, q, k, weights, indices);
+}
+
+// ------------------------------------------------------------------ filter kernel
+
+// Value of the partner lane in a 16-lane sorting stage (p = lane & 15).
+// KIND: 0 = p ^ 1, 1 = p ^ 2 (quad permutes), 2 = p ^ 4 (ds_swizzle, bit mode:
+// and 0x1F, xor 4), 3 = p ^ 3 (quad reverse), 4 = p ^ 7 (row_half_mirror),
+// 5 = p ^ 15 (row_mirror).  The kernel is VALU-bound, and the swizzle runs on
+// the LDS unit where two DPP row shifts and a select would take VALU slots.
+template <int KIND>
+__device__ __forceinline__ uint32_t partner16(uint32_t v) {
+  if constexpr (KIND == 0) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+  if constexpr (KIND == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
+  if constexpr (KIND == 2) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x101F);
+  if constexpr (KIND == 3) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x1B, 0xF, 0xF, false);
+  if constexpr (KIND == 4) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false);
+  if constexpr (KIND == 5) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false);
+}
+
+template <int KIND, int BIT>
+__device__ __forceinline__ int32_t cx_i32(int32_t v, int p) {
+  const int32_t w = (int32_t)partner16<KIND>((uint32_t)v);
+  return (p & BIT) ? (v < w ? v : w) : (v > w ? v : w);
+}
+template <int KIND, int BIT>
+__device__ __forceinline__ uint64_t cx_u64(uint64_t v, int p) {
+  const u32x2 b = __builtin_bit_cast(u32x2, v);
+  const u32x2 o = {partner16<KIND>(b.x), partner16<KIND>(b.y)};
+  const uint64_t w = __builtin_bit_cast(uint64_t, o);
+  return ((v > w) == ((p & BIT) == 0)) ? v : w;
+}
+
+// Descending sort of one value per lane across the 16 lanes of a row (p = lane
+// & 15 ends holding the p-th largest).  Bitonic sort in its mirror form: the
+// first stage of each merge of two sorted blocks compares lane i with its
+// mirror in the merged block, the later stages are half-cleaners at distances
+// 4, 2, 1; the lower lane of each pair keeps the larger value.
+__device__ __forceinline__ int32_t sort16_desc(int32_t v, int p) {
+  v = cx_i32<0, 1>(v, p);
+  v = cx_i32<3, 2>(v, p);
+  v = cx_i32<0, 1>(v, p);
+  v = cx_i32<4, 4>(v, p);
+  v = cx_i32<1, 2>(v, p);
+  v = cx_i32<0, 1>(v, p);
+  v = cx_i32<5, 8>(v, p);
+  v = cx_i32<2, 4>(v, p);
+  v = cx_i32<1, 2>(v, p);
+  return cx_i32<0, 1>(v, p);
+}
+__device__ __forceinline__ uint64_t sort16_desc(uint64_t v, int p) {
+  v = cx_u64<0, 1>(v, p);
+  v = cx_u64<3, 2>(v, p);
+  v = cx_u64<0, 1>(v, p);
+  v = cx_u64<4, 4>(v, p);
+  v = cx_u64<1, 2>(v, p);
+  v = cx_u64<0, 1>(v, p);
+  v = cx_u64<5, 8>(v, p);
+  v = cx_u64<2, 4>(v, p);
+  v = cx_u64<1, 2>(v, p);
+  return cx_u64<0, 1>(v, p);
+}
+
+template <int DT, int V, int KMAX>
+__global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__ logits, void* __restrict__ weights,
+                                                        int32_t* __restrict__ indices, int64_t M, int k) {
+  constexpr int LPR = 16;
+  constexpr int E = LPR * V;
+  constexpr int ESZ = DT == 0 ? 4 : 2;
+  constexpr int ROWB = E * ESZ;                       // bytes per row
+  constexpr int CB = V * ESZ < 16 ? V * ESZ : 16;     // bytes per load
+  constexpr int NC = V * ESZ / CB;                    // loads per lane
+  constexpr int EPC = CB / ESZ;                       // elements per load
+  constexpr int CW = CB / 4;                          // words per load
+  constexpr int ROWS = kBlock / LPR;
+  static_assert(CB == 8 || CB == 16, "filter_kernel: 8- or 16-byte loads");
+
+  __shared__ __attribute__((aligned(16))) uint32_t stage[ROWS][ROWB / 4];
+  __shared__ uint16_t cand[ROWS][LPR];
+
+  const int slot = threadIdx.x / LPR;
+  const int q = threadIdx.x % LPR;
+  const int64_t r = (int64_t)blockIdx.x * ROWS + slot;
+  if (r >= M) return;  // whole rows leave together; every exchange below stays inside a row
+
+  // Load c of lane q covers row elements c*16*EPC + q*EPC + (0 .. EPC-1), so
+  // one load instruction of the row's lanes reads 16*CB contiguous bytes.
+  uint32_t w[NC * CW];
+  {
+    const char* rowp = reinterpret_cast<const char*>(logits) + r * ROWB;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int off = c * LPR * CB + q * CB;
+      if constexpr (CB == 16) {
+        const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rowp + off));
+        *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(stage[slot]) + off) = x;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[c * 4 + i] = x[i];
+      } else {
+        const u32x2 x = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(rowp + off));
+        *reinterpret_cast<u32x2*>(reinterpret_cast<char*>(stage[slot]) + off) = x;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) w[c * 2 + i] = x[i];
+      }
+    }
+  }
+  uint32_t f[V];  // fp32 bits of the lane's elements, j = c*EPC + i
+#pragma unroll
+  for (int j = 0; j < V; ++j) f[j] = f32_bits<DT>(w[j * ESZ / 4], j & 1);
+
+  // 1. lane maximum and minimum in flip-key order
+  int32_t kmax = flip_key(f[0]), kmin = kmax;
+#pragma unroll
+  for (int j = 1; j < V; ++j) {
+    const int32_t kj = flip_key(f[j]);
+    kmax = kmax > kj ? kmax : kj;
+    kmin = kmin < kj ? kmin : kj;
+  }
+  // +inf / +NaN keys are >= flip(0x7F800000); -inf / -NaN keys are <= flip(0xFF800000).
+  const bool finite = kmax < 0x7F800000 && kmin > (int32_t)0x807FFFFFu;
+
+  // 2. T = the k-th largest lane maximum (flip order refines float order, so
+  // the k lanes above it hold k elements that are >= T as floats)
+  const int32_t tkey = __shfl(sort16_desc(kmax, q), k - 1, LPR);
+  const float T = __builtin_bit_cast(float, (uint32_t)flip_key((uint32_t)tkey));
+
+  // 3. candidate mask, bit j for element j
+  uint32_t mask = 0;
+#pragma unroll
+  for (int j = V - 1; j >= 0; --j) mask = mask + mask + (uint32_t)(__builtin_bit_cast(float, f[j]) >= T);
+  const int cnt = __builtin_popcount(mask);
+
+  // inclusive prefix of the counts across the row's 16 lanes
+  int incl = cnt;
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xF, 0xF, true);  // row_shr:1
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, true);  // row_shr:2
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, true);  // row_shr:4
+  incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, true);  // row_shr:8
+  const int total = __shfl(incl, LPR - 1, LPR);
+
+  if (__builtin_amdgcn_ballot_w64(!(finite && total <= LPR)) == 0) {
+    // 4. compact the row's candidates (row indices) into cand[slot]
+    uint32_t mm = mask;
+    int pos = incl - cnt;
+    while (__builtin_amdgcn_ballot_w64(mm != 0)) {
+      if (mm != 0) {
+        const int j = __builtin_ctz(mm);
+        mm &= mm - 1;
+        const int idx = (j / EPC) * (LPR * EPC) + q * EPC + (j % EPC);
+        cand[slot][pos++] = (uint16_t)idx;
+      }
+    }
+    // The list is read by other lanes of this wavefront only (each wavefront
+    // owns its rows' LDS), so a wavefront-scope fence orders the accesses.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // lane q takes candidate q as (key, 1023 - index); 0 marks no candidate
+    uint64_t v = 0;
+    if (q < total) {
+      const int idx = cand[slot][q];
+      const uint32_t word = stage[slot][idx * ESZ / 4];
+      const uint32_t key = key_of_bits(f32_bits<DT>(word, idx & 1));
+      v = ((uint64_t)key << 32) | (uint32_t)(1023 - idx);
+    }
+    v = sort16_desc(v, q);
+
+    // lane t < k holds selection t
+    const float val = float_of_key((uint32_t)(v >> 32));
+    const float v0 = __shfl(val, 0, LPR);
+    const float et = q < k ? expf(val - v0) : 0.f;
+    float e[KMAX];
+#pragma unroll
+    for (int t = 0; t < KMAX; ++t) e[t] = __shfl(et, t, LPR);
+    const float sum = np_sum<KMAX>(e, k);
+    if (q < k) {
+      store_weight<DT>(weights, r * k + q, et / sum);
+      indices[r * k + q] = 1023 - (int)(uint32_t)v;
+    }
+  } else {
+    // exact path on the staged rows: lane q takes elements q*V .. q*V+V-1
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    uint32_t u[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const int idx = q * V + j;
+      u[j] = key_of_bits(f32_bits<DT>(stage[slot][idx * ESZ / 4], idx & 1));
+    }
+    double sel[KMAX];
+    exact_select<V, LPR, KMAX>(u, q, sel);
+    write_selected<DT, LPR, KMAX>(sel, r, q, k, weights, indices);
+  }
+}
+
+template <int DT, int V, int LPR, int KMAX>
 static tb_status launch(const void* logits, void* weights, int32_t* indices, int64_t M, int E, int k,
                         hipStream_t stream) {
   constexpr int ROWS = kBlock / LPR;
@@ -290,12 +556,29 @@ static tb_status launch(const void* logits, void* weights, int32_t* indices, int
   return launch_status("tb_moe_topk_gating");
 }
 
+template <int DT, int V, int KMAX>
+static tb_status launch_filter(const void* logits, void* weights, int32_t* indices, int64_t M, int k,
+                               hipStream_t stream) {
+  constexpr int ROWS = kBlock / 16;
+  const int64_t blocks = (M + ROWS - 1) / ROWS;
+  hipLaunchKernelGGL((filter_kernel<DT, V, KMAX>), dim3((unsigned)blocks), dim3(kBlock), 0, stream, logits, weights,
+                     indices, M, k);
+  return launch_status("tb_moe_topk_gating");
+}
+
 template <int DT, int KMAX>
 static tb_status dispatch_shape(const void* logits, void* weights, int32_t* indices, int64_t M, int E, int k,
                                 hipStream_t stream) {
-  // 16 elements per lane (four 16-byte loads in fp32, two in fp16/bf16) and
-  // as many lanes per row as that takes: measured on E in {64, 128, 256}, 16
-  // per lane beats 8 (more butterfly work per row) and 32 (fewer wavefronts).
+  // Filter kernel: E = 16·V for V in {4, 8, 16} and 2 < k <= 8.  For k <= 2
+  // the exact kernel's two selection rounds cost less than the filter's two
+  // 16-lane sorts (measured on the fp16 E = 128, k = 2 reference grid).
+  if constexpr (KMAX == 8) {
+    if (E == 64) return launch_filter<DT, 4, KMAX>(logits, weights, indices, M, k, stream);
+    if (E == 128) return launch_filter<DT, 8, KMAX>(logits, weights, indices, M, k, stream);
+    if (E == 256) return launch_filter<DT, 16, KMAX>(logits, weights, indices, M, k, stream);
+  }
+  // Exact kernel: 16 elements per lane (four 16-byte loads in fp32, two in
+  // fp16/bf16) and as many lanes per row as that takes.
   if (E <= 16) return launch<DT, 16, 1, KMAX>(logits, weights, indices, M, E, k, stream);
   if (E <= 32) return launch<DT, 16, 2, KMAX>(logits, weights, indices, M, E, k, stream);
   if (E <= 64) return launch<DT, 16, 4, KMAX>(logits, weights, indices, M, E, k, stream);
