@@ -83,7 +83,7 @@ def _w_gating(E):
 
         return dict(name=f"moe_topk_gating_E{E}", config={"workload": "moe_topk_gating", "M": M, "E": E, "k": k},
                     metric="MoE gating HBM throughput", unit="GB/s", dtype="fp32", bound="hbm", bytes=nbytes,
-                    flops=None, inputs=inputs, step=lambda x: impl_hip.run(*x), kernel="tb::gating_kernel<0, 16, 4, 8>" if E <= 64 else "tb::gating_kernel<0, 16, 16, 8>",
+                    flops=None, inputs=inputs, step=lambda x: impl_hip.run(*x), kernel=f"tb::filter_kernel<0, {E // 16}, 8>",
                     cpu_sample=cpu_sample)
     return make
 
