@@ -42,6 +42,7 @@
 #include "tb_common.h"
 
 #include <algorithm>
+#include <type_traits>
 
 #pragma clang fp contract(off)
 
@@ -585,21 +586,29 @@ __global__ void __launch_bounds__(T4, 1)
 // consumed (one unit in flight per wavefront: the chip's loads then arrive
 // early enough for compute to overlap them; deeper prefetch measured slower).
 // Per unit a lane loads an 8 x 16 int4 block (eight 8-byte row loads; 16 lanes
-// side by side cover a full 128-byte line of a row) with its group's scales and
-// zero-points, all buffer loads whose offsets are out of range (zeros, no
-// traffic) where a row, column or unit does not exist, so no load sits behind
-// a branch and the compiler's wait before a unit covers only that unit.  It
-// dequantises exactly as the prefill kernel does, pairs consecutive rows of a
-// column with one byte permute, and feeds sixteen v_mfma_f32_16x16x32_f16
-// (A rows >= M are zero): fragment f holds columns 16c + f, c = lane % 16.  The eight wave partials are summed in LDS in
-// a fixed order, so results are reproducible bit for bit.
+// side by side cover a full 128-byte line of a row) and its A fragment; a
+// group's scales and zero-points are loaded once, at the group's first unit.
+// All are buffer loads whose offsets are out of range (zeros, no traffic) where
+// a row, column or unit does not exist, so no load sits behind a branch and
+// the compiler's wait before a unit covers only that unit.  The MFMAs
+// (v_mfma_f32_16x16x32_f16, A rows >= M zero; fragment f holds columns
+// 16c + f, c = lane % 16) take the codes themselves as 1024 + q, built from
+// the packed bytes by one byte permute per two rows and an and-or per nibble
+// (about one VALU instruction per weight, against 2.4 for dequantising each
+// weight first); the scale and zero-point enter once per group, in fp32:
+// sum_k a (q - z) s = s (sum_k a (1024 + q) - (1024 + z) sum_k a), with the A
+// row sums from one more MFMA against ones.  The weights are therefore not
+// rounded to fp16 before the product (the dense and grouped kernels round
+// them, as the reference dequantisation does); the difference stays far below
+// the 1e-2 tolerance.  The eight wave partials are summed in LDS in a fixed
+// order, so results are reproducible bit for bit.
 // Across the S blocks of a slab the reduction is a serial split-K: each block
 // writes its fp32 partial through to the device-coherent level, then bumps the
 // slab's arrival counter; the block that arrives last reads the S partials
 // (all loads in flight at once), adds them in slot order (deterministic),
 // writes fp16 Y and puts the counter back to zero, so the workspace is ready
 // for the next call without any clearing.
-constexpr int DEC_COLS = 256, DEC_THREADS = 512, DEC_WAVES = 8, DEC_UNIT = 32, DEC_DEPTH = 1, DEC_MAX_SPLITS = 16;
+constexpr int DEC_COLS = 256, DEC_THREADS = 512, DEC_WAVES = 8, DEC_UNIT = 32, DEC_MAX_SPLITS = 16;
 constexpr int AUX_SC1 = 16;  // buffer cache policy: coherent across the XCDs
 // Workspace layout, the same for every shape so that calls of different shapes
 // can share one buffer: [DEC_MAX_SLABS int32 arrival counters][fp32 partials].
@@ -612,8 +621,10 @@ typedef float f32x4d __attribute__((ext_vector_type(4)));
 struct DecUnit {
   u32x2 w[8];  // rows kg*8 + r, columns 16c .. 16c + 15
   u32x4 a;     // A row lane % 16, k = kg*8 .. +7
-  u32x4 s0, s1;  // scales of the unit's group, columns 16c .. 16c + 15
-  uint32_t z0, z1;
+};
+struct DecGroup {
+  u32x4 s0, s1;  // scales of the group, columns 16c .. 16c + 15
+  uint32_t z0, z1;  // zero-points of the group, columns 16c .. 16c + 15
 };
 
 template <bool TAIL>
@@ -661,12 +672,6 @@ __global__ void __launch_bounds__(DEC_THREADS)
   auto load_unit = [&](DecUnit& d, int u) {
     const bool live = u < w_end;
     const uint32_t kw = live ? (uint32_t)(u * DEC_UNIT) * half_n : OOB;
-    const int g = live ? (u * DEC_UNIT) / group : 0;
-    const uint32_t ks = live ? (uint32_t)g * (uint32_t)N * 2u : OOB, kz = live ? (uint32_t)g * half_n : OOB;
-    d.s0 = __builtin_amdgcn_raw_buffer_load_b128(rs, s_off0, ks, 0);
-    d.s1 = __builtin_amdgcn_raw_buffer_load_b128(rs, s_off1, ks, 0);
-    d.z0 = __builtin_amdgcn_raw_buffer_load_b32(rz, z_off0, kz, 0);
-    d.z1 = __builtin_amdgcn_raw_buffer_load_b32(rz, z_off1, kz, 0);
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       d.w[r] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw, w_off + (uint32_t)r * half_n, kw, NT));
@@ -677,46 +682,84 @@ __global__ void __launch_bounds__(DEC_THREADS)
     }
     d.a = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off, live ? (uint32_t)(u * DEC_UNIT) * 2u : OOB, 0);
   };
-  auto compute_unit = [&](const DecUnit& d) {
-    f16x2 zh[2][4], sh[2][4];
-    unpack8x(d.z0, zh[0]);
-    unpack8x(d.z1, zh[1]);
-    scales_x(d.s0, sh[0]);
-    scales_x(d.s1, sh[1]);
+  // A group's scales and zero-points, needed only by its fold.
+  auto load_group = [&](DecGroup& d, int g) {
+    const uint32_t ks = (uint32_t)g * (uint32_t)N * 2u, kz = (uint32_t)g * half_n;
+    d.s0 = __builtin_amdgcn_raw_buffer_load_b128(rs, s_off0, ks, 0);
+    d.s1 = __builtin_amdgcn_raw_buffer_load_b128(rs, s_off1, ks, 0);
+    d.z0 = __builtin_amdgcn_raw_buffer_load_b32(rz, z_off0, kz, 0);
+    d.z1 = __builtin_amdgcn_raw_buffer_load_b32(rz, z_off1, kz, 0);
+  };
+  // One unit's MFMAs on the raw codes: B fragment f holds column 16c + f as
+  // 1024 + q (exact in fp16) for the lane's 8 rows, built straight from the
+  // packed bytes: one byte permute takes byte b of rows 2i and 2i+1, and an
+  // and-or (after a 4-bit shift for the odd column) places the two nibbles
+  // under the 0x6400 exponent, so each half2 is a k-pair of one column.  The
+  // scale and zero-point are applied once per group to the fp32 sums (fold
+  // below); a ninth-row MFMA against ones accumulates the A row sums it needs.
+  const h8 ones = __builtin_bit_cast(h8, u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u});
+  auto mma_unit = [&](const DecUnit& d, f32x4d (&tmp)[16], f32x4d& asum, auto first) {
+    constexpr bool FIRST = decltype(first)::value;
+    const f32x4d zero{};
     const h8 af = __builtin_bit_cast(h8, d.a);
+    asum = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, ones, FIRST ? zero : asum, 0, 0, 0);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      uint32_t dq[8][4];
+      u32x4 col[8];
 #pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        f16x2 hv[4];
-        unpack8x(d.w[r][h], hv);
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t x = d.w[2 * i][h], y = d.w[2 * i + 1][h];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dq[r][j] = as_u32((hv[j] - zh[h][j]) * sh[h][j]);
+        for (int b = 0; b < 4; ++b) {
+          const uint32_t pb = perm(y, x, (uint32_t)b | 0x0C00u | ((uint32_t)(4 + b) << 16) | 0x0C000000u);
+          col[2 * b][i] = (pb & 0x000F000Fu) | 0x64006400u;
+          col[2 * b + 1][i] = ((pb >> 4) & 0x000F000Fu) | 0x64006400u;
+        }
       }
-      // column cc (0..7) of the dword is pair (cc & 1) * 2 + (cc >> 2), half (cc >> 1) & 1
 #pragma unroll
       for (int cc = 0; cc < 8; ++cc) {
-          const int pj = (cc & 1) * 2 + (cc >> 2);
-          const uint32_t sel = ((cc >> 1) & 1) ? 0x07060302u : 0x05040100u;
-          u32x4 col;
+        const int f = h * 8 + cc;
+        tmp[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, __builtin_bit_cast(h8, col[cc]), FIRST ? zero : tmp[f],
+                                                        0, 0, 0);
+      }
+    }
+  };
+  // Fold of one group: sum_k a (q - z) s = s (sum_k a (1024 + q) - (1024 + z) sum_k a),
+  // in fp32, for the rows e < M only (rows past M are never stored).
+  auto fold = [&](const f32x4d (&tmp)[16], const f32x4d& asum, const DecGroup& gp) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) col[q] = perm(dq[2 * q + 1][pj], dq[2 * q][pj], sel);
-          const int f = h * 8 + cc;
-          acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, __builtin_bit_cast(h8, col), acc[f], 0, 0, 0);
-        }
+    for (int f = 0; f < 16; ++f) {
+      const u32x4 sv = f < 8 ? gp.s0 : gp.s1;
+      const float sf = (float)__builtin_bit_cast(_Float16, (uint16_t)(sv[(f % 8) / 2] >> (16 * (f & 1))));
+      const float zf = (float)(1024u + (((f < 8 ? gp.z0 : gp.z1) >> (4 * (f % 8))) & 15u));
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (e < M) acc[f][e] = __builtin_fmaf(sf, __builtin_fmaf(-zf, asum[e], tmp[f][e]), acc[f][e]);
     }
   };
 
-  DecUnit buf[DEC_DEPTH];
-#pragma unroll
-  for (int p = 0; p < DEC_DEPTH; ++p) load_unit(buf[p], w_begin + p);
-  for (int u = w_begin; u < w_end; u += DEC_DEPTH) {
-#pragma unroll
-    for (int p = 0; p < DEC_DEPTH; ++p) {
-      compute_unit(buf[p]);  // a unit past the range holds zeros and adds nothing
-      load_unit(buf[p], u + p + DEC_DEPTH);
+  // The wavefront's units, group by group: the group's scales and zero-points
+  // are loaded at its start, its first unit starts the sums from zero, and
+  // its last is followed by the fold.  The next unit's loads are issued as
+  // soon as a unit's MFMAs have taken its registers (one unit in flight per
+  // wavefront: double buffering measured slower, the weights' stream being
+  // the limit).
+  const int upg = group / DEC_UNIT;
+  DecUnit buf;
+  load_unit(buf, w_begin);
+  int u = w_begin;
+  while (u < w_end) {
+    const int gend = min(w_end, (u / upg + 1) * upg);
+    DecGroup gp;
+    load_group(gp, u / upg);
+    f32x4d tmp[16], asum;
+    mma_unit(buf, tmp, asum, std::true_type{});
+    load_unit(buf, ++u);
+    for (; u < gend; ++u) {
+      mma_unit(buf, tmp, asum, std::false_type{});
+      load_unit(buf, u + 1);
     }
+    fold(tmp, asum, gp);
   }
 
   // Accumulator f, element e: row 4 * (lane / 16) + e, column 16c + f.
