@@ -335,7 +335,7 @@ def _w_matmul_int8():
     return dict(name="matmul_int8", config={"workload": "matmul_int8", "M": M, "N": N, "K": K},
                 metric="matmul_int8 throughput", unit="TFLOP/s", dtype="int8 x int2 -> int32", bound="mfma",
                 peak_key="int8", bytes=nbytes, flops=2 * M * N * K, inputs=inputs, step=lambda x: impl_hip.run(*x),
-                kernel="tb::ntg::nt_gemm<3, 4, 128, 128, 64, 64>", cpu_sample=cpu_sample)
+                kernel="tb::ntg::nt_gemm<3, 4, 256, 256, 128, 64>", cpu_sample=cpu_sample)
 
 
 def _w_matmul(dt):

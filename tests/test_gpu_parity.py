@@ -505,7 +505,9 @@ def _rows(M, n, seed):
 
 
 @pytest.mark.parametrize("M,N,K", [(256, 256, 1024), (100, 264, 512), (2048, 2048, 1024), (2048, 2048, 20480),
-                                   (1024, 1024, 128), (4096, 4096, 1024)])
+                                   (1024, 1024, 128), (4096, 4096, 1024),
+                                   # split-K: 4 splits over 37 K steps with ragged tile edges; 8 splits
+                                   (600, 520, 4736), (256, 512, 16384)])
 def test_matmul_int8_bit_exact(gpu, M, N, K):
     from tilebench_amd.benchmarks.operators.matmul_int8 import impl_hip
 
@@ -515,6 +517,8 @@ def test_matmul_int8_bit_exact(gpu, M, N, K):
     torch.cuda.synchronize()
     rows = _rows(M, 128, K)
     np.testing.assert_array_equal(out.cpu().numpy()[rows], oracle.matmul_int8(a.numpy()[rows], b.numpy()))
+    splits = impl_hip.get_last_config()["k_splits"]
+    assert splits == {(2048, 2048, 20480): 4, (600, 520, 4736): 4, (256, 512, 16384): 8}.get((M, N, K), 1)
 
 
 @pytest.mark.parametrize("M,N,K", [(512, 512, 1024), (300, 136, 256), (4096, 4096, 4096)])

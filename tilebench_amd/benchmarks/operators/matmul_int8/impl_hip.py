@@ -21,8 +21,24 @@ def run(a: torch.Tensor, b: torch.Tensor, **kwargs):
     ws = torch.empty(need, dtype=torch.uint8, device=a.device)
     rt.call("tb_matmul_int8", a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, ws.data_ptr(), need,
             rt.stream_handle(a.device))
+    global _last_config
+    _last_config = _config(M, N, K)
     return out
 
 
+def _config(M, N, K):
+    """The kernel choice of tb_matmul_int8 (nt_gemm.hip: big_tiles, int8_splits)."""
+    tiles256 = -(-M // 256) * -(-N // 256)
+    if tiles256 >= 256:
+        return {"kernel": "nt_gemm<i8>", "tile": "256x256", "k_splits": 1}
+    splits = min(8, 256 // tiles256, K // 128 // 8)
+    if splits >= 2:
+        return {"kernel": "nt_gemm<i8>", "tile": "256x256", "k_splits": splits}
+    return {"kernel": "nt_gemm<i8>", "tile": "128x128", "k_splits": 1}
+
+
+_last_config = None
+
+
 def get_last_config():
-    return {"kernel": "nt_gemm<i8>", "tile": "128x128"}
+    return _last_config

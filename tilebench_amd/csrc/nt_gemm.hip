@@ -20,8 +20,12 @@
 // The MFMA takes the B^T fragment as its first operand, so each lane ends with
 // four consecutive output columns per accumulator group and stores them
 // straight from registers.  Two tile shapes: 256 x 256 on eight wavefronts
-// (128 x 64 each) and 128 x 128 on four (64 x 64 each), for the M = N = 2048
-// grid of matmul_int8 (256 tiles, one per CU).
+// (128 x 64 each) and 128 x 128 on four (64 x 64 each) for grids too small for
+// 256 x 256 tiles.  matmul_int8 at M = N = 2048 (64 tiles of 256 x 256) splits
+// K instead when K is deep: 128 x 128 int8 tiles need 32 KiB of operands per
+// CU per 128-byte K step, about the L2-to-CU bandwidth at the MFMA rate, where
+// 256 x 256 tiles need half that per MAC; each split writes an int32 partial
+// plane and a pass adds the planes (exact, so the split does not change a bit).
 //
 // fp32 without an fp32-rate penalty: x = hi + lo with hi = bf16(x) and
 // lo = bf16(x - hi) (x - hi is exact in fp32), and
@@ -75,10 +79,9 @@ __device__ __forceinline__ void dma16(uint32_t lds_addr, uint32_t voff, const i3
 }
 
 template <int BM, int BN>
-__device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int& m0, int& n0) {
+__device__ __forceinline__ void tile_of_block(int bid, int tiles_m, int tiles_n, int& m0, int& n0) {
   constexpr int GROUP_M = 8;
   const int nb = tiles_m * tiles_n;
-  int bid = blockIdx.x;
   if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);  // contiguous run of tiles per XCD
   const int per_group = GROUP_M * tiles_n;
   const int group = bid / per_group;
@@ -119,7 +122,7 @@ template <int KIND, int OUT, int BM, int BN, int WM, int WN>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64, 1)
     nt_gemm(const uint8_t* __restrict__ A, const uint8_t* __restrict__ BT, void* __restrict__ Yv,
             const float* __restrict__ sa, const float* __restrict__ sw, int M, int N, int Kb, int tiles_m,
-            int tiles_n) {
+            int tiles_n, int splits) {
   constexpr int WAVES = (BM / WM) * (BN / WN), THREADS = WAVES * 64;
   constexpr int FI = WM / 32, FJ = WN / 32;
   constexpr int A_STAGE = BM * BK, B_STAGE = BN * BK;
@@ -128,8 +131,17 @@ __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64, 1)
   static_assert(A_DMA * WAVES * 8 == BM && B_DMA * WAVES * 8 == BN, "tile rows must split evenly over the DMA");
   typedef typename Acc<KIND>::type acc_t;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  // Split-K (int32 output only): block b computes K steps [split * nk / splits,
+  // (split + 1) * nk / splits), split = b / tiles, of tile b % tiles into
+  // partial plane `split` of Yv (each plane M x N); a reduction pass adds the
+  // planes (int32 sums are exact in any order, so the result equals the
+  // unsplit product bit for bit).  Each split's blocks are consecutive, so the
+  // per-XCD tile grouping below sees the same block ids as without splits.
+  const int tiles = tiles_m * tiles_n;
+  const int split = (int)blockIdx.x / tiles;
   int m0, n0;
-  tile_of_block<BM, BN>(tiles_m, tiles_n, m0, n0);
+  tile_of_block<BM, BN>((int)blockIdx.x % tiles, tiles_m, tiles_n, m0, n0);
+  if constexpr (OUT == OUT_I32) Yv = reinterpret_cast<int32_t*>(Yv) + (int64_t)split * M * N;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave / (BN / WN), wn = wave % (BN / WN);
 
@@ -153,8 +165,9 @@ __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64, 1)
   }
   const uint32_t lds0 = (uint32_t)__builtin_amdgcn_readfirstlane(
       (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
+  int k_first = 0;  // first K step of this block (stage parity counts from it)
   auto issue = [&](int kt) {
-    const uint32_t st = lds0 + (uint32_t)((kt & 1) * (A_STAGE + B_STAGE));
+    const uint32_t st = lds0 + (uint32_t)(((kt - k_first) & 1) * (A_STAGE + B_STAGE));
     const uint32_t soff = (uint32_t)(kt * BK);
 #pragma unroll
     for (int i = 0; i < A_DMA; ++i) dma16(st + (uint32_t)((wave * A_DMA + i) * 1024), a_off[i], ra, soff);
@@ -188,14 +201,16 @@ __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64, 1)
     for (int j = 0; j < FJ; ++j) acc[i][j] = acc_t{};
 
   constexpr int WAIT_VM0 = 0 | (7 << 4) | (15 << 8);
-  const int nk = Kb / BK;
-  issue(0);
+  const int nk_all = Kb / BK;
+  const int k_begin = (int)((int64_t)nk_all * split / splits), k_end = (int)((int64_t)nk_all * (split + 1) / splits);
+  k_first = k_begin;
+  issue(k_begin);
   __builtin_amdgcn_s_waitcnt(WAIT_VM0);
   __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const bool more = kt + 1 < nk;
+  for (int kt = k_begin; kt < k_end; ++kt) {
+    const bool more = kt + 1 < k_end;
     if (more) issue(kt + 1);
-    const uint8_t* sa_ = lds + (kt & 1) * (A_STAGE + B_STAGE);
+    const uint8_t* sa_ = lds + ((kt - k_begin) & 1) * (A_STAGE + B_STAGE);
     const uint8_t* sb_ = sa_ + A_STAGE;
     if constexpr (KIND == KIND_FP8) {
       // Both k64 substeps' fragments are read up front; the scheduling hints
@@ -483,15 +498,37 @@ __global__ void __launch_bounds__(256) split_transpose(const float* __restrict__
 
 template <int KIND, int OUT, int BM, int BN, int WM, int WN>
 tb_status launch_nt(const uint8_t* A, const uint8_t* BT, void* Y, const float* sa, const float* sw, int64_t M,
-                    int64_t N, int64_t Kb, hipStream_t stream, const char* what) {
+                    int64_t N, int64_t Kb, hipStream_t stream, const char* what, int splits = 1) {
   auto kern = &nt_gemm<KIND, OUT, BM, BN, WM, WN>;
   constexpr size_t lds = (size_t)2 * (BM + BN) * BK;
   if (tb_status st = reserve_lds(reinterpret_cast<const void*>(kern), lds, what)) return st;
   const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
   constexpr int threads = (BM / WM) * (BN / WN) * 64;
-  hipLaunchKernelGGL(kern, dim3(tiles_m * tiles_n), dim3(threads), lds, stream, A, BT, Y, sa, sw, (int)M, (int)N,
-                     (int)Kb, tiles_m, tiles_n);
+  hipLaunchKernelGGL(kern, dim3(tiles_m * tiles_n * splits), dim3(threads), lds, stream, A, BT, Y, sa, sw, (int)M,
+                     (int)N, (int)Kb, tiles_m, tiles_n, splits);
   return launch_status(what);
+}
+
+// Sum of the `splits` int32 partial planes of n elements (n % 4 == 0), in
+// plane order, one 16-byte chunk per thread.
+__global__ void __launch_bounds__(256) reduce_planes_i32(const i32x4* __restrict__ planes, i32x4* __restrict__ out,
+                                                         int64_t n4, int splits) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  i32x4 s = __builtin_nontemporal_load(planes + i);
+  for (int p = 1; p < splits; ++p) s += __builtin_nontemporal_load(planes + (int64_t)p * n4 + i);
+  out[i] = s;
+}
+
+// K splits for the int8 GEMM: 256 x 256 tiles with enough splits to give the
+// device about one block per CU, when the 256 x 256 grid alone is too small
+// and K is deep enough (at least 8 steps of 128 per split); 1 = no split.
+inline int int8_splits(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
+  if (tiles >= 256) return 1;
+  int64_t s = std::min<int64_t>(8, 256 / tiles);
+  s = std::min<int64_t>(s, K / BK / 8);
+  return s >= 2 ? (int)s : 1;
 }
 
 // 256 x 256 tiles when they alone fill the device, else 128 x 128.
@@ -510,7 +547,12 @@ extern "C" tb_status tb_matmul_workspace_size(int dtype, int64_t M, int64_t N, i
     case 0: *bytes = 6 * K * (M + N); break;  // A' and B'^T, bf16, 3K wide
     case 1: *bytes = 2 * K * N; break;        // B^T fp16
     case 2: *bytes = K * N; break;            // B^T e4m3
-    default: *bytes = K * N; break;           // unpacked B^T int8
+    default: {                                // unpacked B^T int8, then the split-K partial planes
+      *bytes = (K * N + 255) & ~(int64_t)255;
+      const int splits = int8_splits(M, N, K);
+      if (splits > 1) *bytes += (int64_t)splits * M * N * 4;
+      break;
+    }
   }
   *bytes = (*bytes + 255) & ~(int64_t)255;
   return TB_OK;
@@ -603,6 +645,18 @@ extern "C" tb_status tb_matmul_int8(const int8_t* a, const uint8_t* b, int32_t* 
   int8_t* bt = reinterpret_cast<int8_t*>(workspace);
   hipLaunchKernelGGL(unpack_i2_tile, dim3((unsigned)((N + 63) / 64), (unsigned)((K / 4 + 63) / 64)), dim3(256), 0,
                      stream, b, bt, (int)K, (int)N);
+  const int splits = int8_splits(M, N, K);
+  if (splits > 1) {
+    int32_t* planes = reinterpret_cast<int32_t*>(reinterpret_cast<uint8_t*>(workspace) + ((K * N + 255) & ~(int64_t)255));
+    if (tb_status st = launch_nt<KIND_I8, OUT_I32, 256, 256, 128, 64>(
+            reinterpret_cast<const uint8_t*>(a), reinterpret_cast<const uint8_t*>(bt), planes, nullptr, nullptr, M, N,
+            K, stream, "tb_matmul_int8", splits))
+      return st;
+    const int64_t n4 = M * N / 4;
+    hipLaunchKernelGGL(reduce_planes_i32, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream,
+                       reinterpret_cast<const i32x4*>(planes), reinterpret_cast<i32x4*>(out), n4, splits);
+    return tb::launch_status("tb_matmul_int8(reduce)");
+  }
   if (big_tiles(M, N))
     return launch_nt<KIND_I8, OUT_I32, 256, 256, 128, 64>(reinterpret_cast<const uint8_t*>(a),
                                                           reinterpret_cast<const uint8_t*>(bt), out, nullptr, nullptr,
