@@ -137,10 +137,22 @@ __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64, 1)
   // planes (int32 sums are exact in any order, so the result equals the
   // unsplit product bit for bit).  Each split's blocks are consecutive, so the
   // per-XCD tile grouping below sees the same block ids as without splits.
+  // With splits dividing the 8 XCDs (blocks go round-robin over them), split
+  // s runs on XCDs s*G .. s*G+G-1 (G = 8 / splits) and each of those takes a
+  // contiguous run of tile columns, so an XCD's L2 holds its K range of every
+  // A row panel once and of its own B column panels only.
   const int tiles = tiles_m * tiles_n;
-  const int split = (int)blockIdx.x / tiles;
-  int m0, n0;
-  tile_of_block<BM, BN>((int)blockIdx.x % tiles, tiles_m, tiles_n, m0, n0);
+  int split, m0, n0;
+  if (splits > 1 && 8 % splits == 0 && tiles % (8 / splits) == 0) {
+    const int G = 8 / splits, xcd = (int)blockIdx.x & 7, j = (int)blockIdx.x >> 3;
+    split = xcd / G;
+    const int t = (xcd % G) * (tiles / G) + j;  // column-major over the split's tiles
+    m0 = (t % tiles_m) * BM;
+    n0 = (t / tiles_m) * BN;
+  } else {
+    split = (int)blockIdx.x / tiles;
+    tile_of_block<BM, BN>((int)blockIdx.x % tiles, tiles_m, tiles_n, m0, n0);
+  }
   if constexpr (OUT == OUT_I32) Yv = reinterpret_cast<int32_t*>(Yv) + (int64_t)split * M * N;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave / (BN / WN), wn = wave % (BN / WN);
