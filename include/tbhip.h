@@ -228,7 +228,10 @@ tb_status tb_quantize_global(const float* x, uint16_t* y, int64_t n, hipStream_t
  * tb_matmul_int8: out int32 [M, N] = a int8 [M, K] @ B, where b uint8 [K/4, N]
  *   holds four 2-bit fields per byte and row i*K/4 + kb of B is
  *   ((b[kb, :] >> 2i) & 3) - 1.  Exact integer arithmetic.  Needs K % 128 == 0,
- *   N % 8 == 0 and a workspace of tb_matmul_workspace_size(3, ...) bytes.
+ *   N % 8 == 0 and a workspace of tb_matmul_workspace_size(3, ...) bytes (the
+ *   unpacked operand, plus int32 partial planes when the GEMM splits K: grids
+ *   of fewer than 256 tiles of 256 x 256 with K >= 2048; every byte it reads
+ *   is written by the same call, so it needs no clearing).
  *   Replaces: matmul_int8/impl_triton.py:118 run(a, b) (semantics impl_torch.py:4-19).
  * tb_matmul: dtype 0 fp32, 1 fp16, 2 fp8-e4m3; a [M, K], b [K, N] and out
  *   [M, N] of that dtype.  fp16: fp16(a @ b) with fp32 accumulation.  fp8:
