@@ -290,7 +290,7 @@ def _w_dequantize_rowwise():
     return dict(name="dequantize_rowwise", config={"workload": "dequantize_rowwise", "rows": rows, "cols": cols},
                 metric="dequantize_rowwise HBM throughput", unit="GB/s", dtype="int8->fp16", bound="hbm",
                 bytes=nbytes, flops=2 * rows * cols, inputs=inputs, step=lambda x: impl_hip.run(*x),
-                kernel="tb::analog::dequant_rowwise_vec", cpu_sample=cpu_sample)
+                kernel="tb::analog::dequant_rowwise_rows", cpu_sample=cpu_sample)
 
 
 def _w_quantize_global():

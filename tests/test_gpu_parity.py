@@ -475,7 +475,8 @@ def test_weight_dequant_matches_oracle(gpu, M, N, tile_size, dt):
                                       ref.view(np.uint32 if dt == "fp32" else np.uint16))
 
 
-@pytest.mark.parametrize("rows,cols", [(512, 512), (4096, 8192), (33, 100), (7, 16)])
+@pytest.mark.parametrize("rows,cols", [(512, 512), (4096, 8192), (33, 100), (7, 16),
+                                       (3, 6160), (65543, 32)])   # a chunk ending in its second half; > 65535 rows
 def test_dequantize_rowwise_matches_oracle(gpu, rows, cols):
     from tilebench_amd.benchmarks.operators.dequantize_rowwise import impl_hip
 

@@ -115,6 +115,33 @@ __global__ void __launch_bounds__(256) dequant_rowwise_vec(const int8_t* __restr
   st_nt(dst + 1, o[1]);
 }
 
+// One row per blockIdx.y, 4096 elements per block: thread t converts elements
+// t*8 .. t*8+7 and 2048 + t*8 .. +7 of the chunk, so each 8-byte load and each
+// 16-byte store instruction of a wavefront covers one contiguous span (512 B
+// read, 1 KiB written), and no thread divides to find its row.
+__global__ void __launch_bounds__(256) dequant_rowwise_rows(const int8_t* __restrict__ x, const float* __restrict__ state,
+                                                            uint16_t* __restrict__ y, int64_t cols) {
+  const int64_t r = blockIdx.y;
+  const float s = state[r];
+  const float inv127 = 1.0f / 127.0f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t c = (int64_t)blockIdx.x * 4096 + h * 2048 + threadIdx.x * 8;
+    if (c >= cols) continue;  // cols % 16 == 0: a thread's 8 elements are all in or all out
+    const u32x2 xv = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(x + r * cols + c));
+    u32x4 o;
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int b = 0; b < 4; b += 2) {
+        const float a0 = (s * (float)(int8_t)((xv[q] >> (8 * b)) & 0xFFu)) * inv127;
+        const float a1 = (s * (float)(int8_t)((xv[q] >> (8 * (b + 1))) & 0xFFu)) * inv127;
+        o[q * 2 + (b >> 1)] = (uint32_t)f_to_h_of_rounded(a0) | ((uint32_t)f_to_h_of_rounded(a1) << 16);
+      }
+    st_nt(reinterpret_cast<u32x4*>(y + r * cols + c), o);
+  }
+}
+
 __global__ void __launch_bounds__(256) dequant_rowwise_scalar(const int8_t* __restrict__ x, const float* __restrict__ state,
                                                               uint16_t* __restrict__ y, int64_t rows, int64_t cols) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -124,16 +151,20 @@ __global__ void __launch_bounds__(256) dequant_rowwise_scalar(const int8_t* __re
 }
 
 // ---------------------------------------------------------------- quantize_global
-__global__ void __launch_bounds__(256) f32_to_f16_vec(const f32x4* __restrict__ x, u32x4* __restrict__ y, int64_t n8) {
-  const int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (v >= n8) return;
-  const f32x4 a = __builtin_nontemporal_load(x + 2 * v), b = __builtin_nontemporal_load(x + 2 * v + 1);
-  u32x4 o;
-  o[0] = (uint32_t)f_to_h(a[0]) | ((uint32_t)f_to_h(a[1]) << 16);
-  o[1] = (uint32_t)f_to_h(a[2]) | ((uint32_t)f_to_h(a[3]) << 16);
-  o[2] = (uint32_t)f_to_h(b[0]) | ((uint32_t)f_to_h(b[1]) << 16);
-  o[3] = (uint32_t)f_to_h(b[2]) | ((uint32_t)f_to_h(b[3]) << 16);
-  st_nt(y + v, o);
+// Groups of 4 elements; thread t of a block converts groups b*512 + t and
+// b*512 + 256 + t, so each 16-byte load and each 8-byte store instruction of a
+// wavefront covers one contiguous span.
+__global__ void __launch_bounds__(256) f32_to_f16_vec(const f32x4* __restrict__ x, u32x2* __restrict__ y, int64_t n4) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t g = (int64_t)blockIdx.x * 512 + h * 256 + threadIdx.x;
+    if (g >= n4) continue;
+    const f32x4 a = __builtin_nontemporal_load(x + g);
+    u32x2 o;
+    o[0] = (uint32_t)f_to_h(a[0]) | ((uint32_t)f_to_h(a[1]) << 16);
+    o[1] = (uint32_t)f_to_h(a[2]) | ((uint32_t)f_to_h(a[3]) << 16);
+    __builtin_nontemporal_store(o, y + g);
+  }
 }
 
 __global__ void __launch_bounds__(256) f32_to_f16_tail(const float* __restrict__ x, uint16_t* __restrict__ y,
@@ -180,7 +211,10 @@ extern "C" tb_status tb_dequantize_rowwise(const int8_t* x, const float* state, 
   TB_CHECK_ARG(x && state && y, "tb_dequantize_rowwise: null pointer");
   TB_CHECK_ARG(rows > 0 && cols > 0 && rows * cols < (1ll << 40), "tb_dequantize_rowwise: bad shape");
   const bool vec = cols % 16 == 0 && tb::aligned(x, 16) && tb::aligned(y, 16);
-  if (vec)
+  if (vec && rows <= 65535)
+    hipLaunchKernelGGL(dequant_rowwise_rows, dim3((unsigned)((cols + 4095) / 4096), (unsigned)rows), dim3(256), 0,
+                       stream, x, state, y, cols);
+  else if (vec)
     hipLaunchKernelGGL(dequant_rowwise_vec, dim3(blocks_for(rows * (cols / 16))), dim3(256), 0, stream, x, state, y,
                        rows, cols);
   else
@@ -193,10 +227,10 @@ extern "C" tb_status tb_quantize_global(const float* x, uint16_t* y, int64_t n, 
   TB_CHECK_ARG(x && y && n > 0 && n < (1ll << 40), "tb_quantize_global: bad arguments");
   int64_t done = 0;
   if (tb::aligned(x, 16) && tb::aligned(y, 16) && n >= 8) {
-    const int64_t n8 = n / 8;
-    hipLaunchKernelGGL(f32_to_f16_vec, dim3(blocks_for(n8)), dim3(256), 0, stream,
-                       reinterpret_cast<const tb::f32x4*>(x), reinterpret_cast<tb::u32x4*>(y), n8);
-    done = n8 * 8;
+    const int64_t n4 = n / 8 * 2;
+    hipLaunchKernelGGL(f32_to_f16_vec, dim3((unsigned)((n4 + 511) / 512)), dim3(256), 0, stream,
+                       reinterpret_cast<const tb::f32x4*>(x), reinterpret_cast<tb::u32x2*>(y), n4);
+    done = n4 * 4;
   }
   if (done < n)
     hipLaunchKernelGGL(f32_to_f16_tail, dim3(blocks_for(n - done)), dim3(256), 0, stream, x, y, done, n);
