@@ -49,7 +49,8 @@ def int4_dequant(packed: np.ndarray, scales: np.ndarray, zeros: np.ndarray, grou
     if s.shape != (K // group, N) or z.shape != (K // group, N):
         raise ValueError("scales / zeros must be [K/G, N]")
     d = (q.reshape(K // group, group, N) - z[:, None, :]).astype(np.float32)
-    return (d * s[:, None, :]).astype(np.float16).reshape(K, N)
+    with np.errstate(over="ignore"):  # products past the fp16 range round to inf, as the cast defines
+        return (d * s[:, None, :]).astype(np.float16).reshape(K, N)
 
 
 # ----------------------------------------------------------------------------- bf16 helpers
@@ -203,8 +204,9 @@ def moe_topk_gating(logits: np.ndarray, k: int, dtype: str = "fp32"):
     v = np.where(isnan, 0.0, x).astype(np.float64) + 0.0  # + 0.0 folds -0.0 onto +0.0
     order = np.lexsort((idx, -v, ~isnan), axis=-1)[:, :k]
     vals = np.take_along_axis(x, order, axis=1).astype(np.float32)
-    e = np.exp(vals - vals[:, :1]).astype(np.float32)
-    w = (e / e.sum(axis=1, keepdims=True, dtype=np.float32)).astype(np.float32)
+    with np.errstate(invalid="ignore"):  # rows holding inf - inf or NaN give NaN weights (IEEE arithmetic)
+        e = np.exp(vals - vals[:, :1]).astype(np.float32)
+        w = (e / e.sum(axis=1, keepdims=True, dtype=np.float32)).astype(np.float32)
     if dtype == "fp16":
         w = w.astype(np.float16)
     elif dtype == "bf16":
