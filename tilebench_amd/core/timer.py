@@ -41,16 +41,13 @@ def _flush_l2_buffer_mb() -> int:
 def flush_l2_cache(flush_mb: int | None = None) -> None:
     """Enqueue a store sweep over the eviction buffer on the current stream
     (asynchronous; the next kernel on the stream starts with a cold cache)."""
+    from tilebench_amd import runtime as rt
+
     global _flush_buf
     nbytes = (flush_mb or _flush_l2_buffer_mb()) * 1024 * 1024
     if _flush_buf is None or _flush_buf.numel() * 4 != nbytes:
         _flush_buf = torch.empty(nbytes // 4, device="cuda", dtype=torch.float32)
-    try:
-        from tilebench_amd import runtime as rt
-
-        rt.call("tb_l2_flush", _flush_buf.data_ptr(), nbytes, 0x3F800000, rt.stream_handle())
-    except ImportError:
-        _flush_buf.fill_(1.0)
+    rt.call("tb_l2_flush", _flush_buf.data_ptr(), nbytes, 0x3F800000, rt.stream_handle())
 
 
 def effective_use_cuda_graph(requested: bool) -> bool:
