@@ -12,7 +12,9 @@ no step finds its operands in the last-level cache.  Prints ONE JSON line with t
 
   roofline      achieved GB/s or TFLOP/s of the operator's kernel (algorithmic
                 bytes or flops per launch / mean launch time from the events),
-                MI355X's published peak and the fraction;
+                MI355X's published peak and the fraction, and the peak this
+                GPU reaches in the same process (measured_peak: the copy or
+                MFMA probe of the library) with the fraction of it;
   cpu_baseline  the numpy CPU oracle timed on the host cores on a bounded slice
                 of the same workload (the oracle is used only as this timed CPU
                 port, never on the GPU path);
@@ -491,6 +493,51 @@ def measured_traffic(kernel: str):
     return None if k is None else int(k["fetch_bytes"] + k["write_bytes"])
 
 
+_MEASURED_PEAKS: dict = {}
+
+
+def measured_peak(bound: str, peak_key: str | None):
+    """The peak this GPU reaches now, measured in this process with the
+    library's probes: HBM GB/s from tb_probe_copy over 512 MiB each way, matrix
+    TFLOP/s from tb_probe_mfma (fp16 32x32x16 or fp8 32x32x64 MFMAs back to back,
+    two 4-wavefront blocks per CU).  None for a matrix type the probe does not
+    cover (int8, fp32).  Each figure is the mean of 10 back-to-back launches
+    after 3 untimed ones, measured once per process."""
+    import torch
+    from tilebench_amd import runtime as rt
+
+    key = "hbm" if bound == "hbm" else peak_key
+    if key in _MEASURED_PEAKS:
+        return _MEASURED_PEAKS[key]
+    stream = rt.stream_handle()
+    if key == "hbm":
+        n = 512 * 1024 * 1024
+        src = torch.empty(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        launch = lambda: rt.call("tb_probe_copy", src.data_ptr(), dst.data_ptr(), n, stream)  # noqa: E731
+        work, scale = 2 * n, 1e9
+    elif key in ("fp16", "fp8"):
+        kind = 0 if key == "fp16" else 1
+        blocks, iters = 2 * torch.cuda.get_device_properties(0).multi_processor_count, 2000
+        out = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+        launch = lambda: rt.call("tb_probe_mfma", kind, blocks, iters, out.data_ptr(), stream)  # noqa: E731
+        work, scale = blocks * 4 * 8 * iters * (32768 if kind == 0 else 131072), 1e12
+    else:
+        _MEASURED_PEAKS[key] = None
+        return None
+    for _ in range(3):
+        launch()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        launch()
+    e1.record()
+    torch.cuda.synchronize()
+    _MEASURED_PEAKS[key] = round(work / (e0.elapsed_time(e1) / 10 * 1e-3) / scale, 2)
+    return _MEASURED_PEAKS[key]
+
+
 def roofline(w, ms: float) -> dict:
     if w["bound"] == "hbm":
         achieved = w["bytes"] / (ms * 1e-3) / 1e9
@@ -498,9 +545,11 @@ def roofline(w, ms: float) -> dict:
     else:
         achieved = w["flops"] / (ms * 1e-3) / 1e12
         peak, unit = PEAK_TFLOPS[w["peak_key"]], "TFLOP/s"
+    mp = measured_peak(w["bound"], w.get("peak_key"))
     return {"bound": w["bound"], "achieved": round(achieved, 2), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": measured_traffic(w["kernel"]),
-            "kernel": w["kernel"]}
+            "kernel": w["kernel"], "measured_peak": mp,
+            "frac_of_measured": None if mp is None else round(achieved / mp, 4)}
 
 
 def cpu_baseline(w, budget_s: float = 10.0) -> dict:
