@@ -164,12 +164,18 @@ __device__ __forceinline__ _Float16 h_of_rounded(float f) {
 //                       at row rm.ids[m] of Y through the staged tile (whole
 //                       512-byte row segments; 8-byte stores straight from the
 //                       accumulators measured 13 % slower).
-template <int AR, int EPI>
+template <int AR, int EPI, bool NW = false>
 __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _Float16* __restrict__ A,
                                              const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
                                              const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int a_rows,
                                              int m0, int m_end, int n0, int N, int K, int group,
                                              const RowMap rm = RowMap{}) {
+  static_assert(!NW || EPI != EPI_SILU_MUL, "prefill_tile: narrow tiles use the plain column mapping");
+  // NW (narrow): the tile's columns are n0 .. n0 + 127 (a last tile of at most
+  // 128 columns); each wavefront owns 32 of them (one B fragment instead of
+  // two) and each thread dequantises 2 rows x 8 columns instead of 4 x 8.
+  constexpr int NJ = NW ? 1 : 2;    // 32-column B fragments per wavefront
+  constexpr int RPT = NW ? 2 : 4;   // W rows per dequantising thread
   _Float16* const lds_a = lds;
   _Float16* const lds_b = lds + A_STAGES * A_STAGE;
   const Tile tile{m0, n0};
@@ -219,8 +225,8 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
   const uint32_t a_lds0 = (uint32_t)__builtin_amdgcn_readfirstlane(
       (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_a) + (uint32_t)(wave * 4 * 1024);
 
-  // W: thread owns rows kq*4 .. kq*4+3 of the 64-row step, columns cg*8 .. +7.
-  const int cg = t & 31, kq = t >> 5;
+  // W: thread owns rows kq*RPT .. kq*RPT+RPT-1 of the 64-row step, columns cg*8 .. +7.
+  const int cg = NW ? (t & 15) : (t & 31), kq = NW ? (t >> 4) : (t >> 5);
   int n = tile.n0 + cg * 8;
   bool n_ok = n < N;
   if (EPI == EPI_SILU_MUL) {
@@ -229,16 +235,17 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
     n_ok = a0 < half_cols;
   }
   const uint32_t w_row = (uint32_t)(N / 2);
-  const uint32_t w_off = n_ok ? (uint32_t)(kq * 4) * w_row + (uint32_t)(n / 2) : OOB;
+  const uint32_t w_off = n_ok ? (uint32_t)(kq * RPT) * w_row + (uint32_t)(n / 2) : OOB;
   const uint32_t s_off = n_ok ? (uint32_t)n * 2u : OOB;
   const uint32_t z_off = n_ok ? (uint32_t)(n / 2) : OOB;
   int b_st[8];
 #pragma unroll
-  for (int c = 0; c < 8; ++c) b_st[c] = swz2(cg * 8 + c, kq >> 1) + (kq & 1) * 4;
+  for (int c = 0; c < 8; ++c)
+    b_st[c] = NW ? swz2(cg * 8 + c, kq >> 2) + (kq & 3) * 2 : swz2(cg * 8 + c, kq >> 1) + (kq & 1) * 4;
 
   // fragment read offsets (halfs) for k16 step ks and row parity of the fragment index
   const int fa_base = (wm * 128 + (lane & 31)) * 64;
-  const int fb_base = (wn * 64 + (lane & 31)) * 64;
+  const int fb_base = (wn * 32 * NJ + (lane & 31)) * 64;
   int fx[4][2];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
@@ -264,7 +271,7 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
     const uint32_t k0 = (uint32_t)(kt * BK);
     const uint32_t kw = k0 * w_row;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) r.w[q] = __builtin_amdgcn_raw_buffer_load_b32(rw, w_off + q * w_row, kw, 0);
+    for (int q = 0; q < RPT; ++q) r.w[q] = __builtin_amdgcn_raw_buffer_load_b32(rw, w_off + q * w_row, kw, 0);
     const uint32_t g = k0 / (uint32_t)group;
     r.s = __builtin_amdgcn_raw_buffer_load_b128(rs, s_off, g * (uint32_t)N * 2u, 0);
     r.z = __builtin_amdgcn_raw_buffer_load_b32(rz, z_off, g * w_row, 0);
@@ -275,7 +282,7 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
     scales_x(r.s, sh);
     uint32_t d[4][4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < RPT; ++q) {
       f16x2 h[4];
       unpack8x(r.w[q], h);
 #pragma unroll
@@ -286,10 +293,14 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
     for (int cc = 0; cc < 8; ++cc) {
       const int pj = (cc & 1) * 2 + (cc >> 2);
       const uint32_t sel = ((cc >> 1) & 1) ? 0x07060302u : 0x05040100u;
-      u32x2v col;
-      col[0] = perm(d[1][pj], d[0][pj], sel);
-      col[1] = perm(d[3][pj], d[2][pj], sel);
-      *reinterpret_cast<u32x2v*>(st + b_st[cc]) = col;
+      if constexpr (NW) {
+        *reinterpret_cast<uint32_t*>(st + b_st[cc]) = perm(d[1][pj], d[0][pj], sel);
+      } else {
+        u32x2v col;
+        col[0] = perm(d[1][pj], d[0][pj], sel);
+        col[1] = perm(d[3][pj], d[2][pj], sel);
+        *reinterpret_cast<u32x2v*>(st + b_st[cc]) = col;
+      }
     }
   };
 
@@ -305,8 +316,11 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
   auto read_frags = [&](const _Float16* sa, const _Float16* sb, int ks, h8 (&fa)[4], h8 (&fb)[2]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) fa[i] = *reinterpret_cast<const h8*>(sa + fa_base + i * 32 * 64 + fx[ks][i & 1]);
+    // The swizzle of LDS row R depends on bit 5 of R: R = wn * 64 + j * 32 + lane % 32
+    // has it from j, a narrow tile's R = wn * 32 + lane % 32 from wn.
 #pragma unroll
-    for (int j = 0; j < 2; ++j) fb[j] = *reinterpret_cast<const h8*>(sb + fb_base + j * 32 * 64 + fx[ks][j & 1]);
+    for (int j = 0; j < NJ; ++j)
+      fb[j] = *reinterpret_cast<const h8*>(sb + fb_base + j * 32 * 64 + fx[ks][NW ? (wn & 1) : (j & 1)]);
   };
   auto mfma_stage = [&](const _Float16* sa, const _Float16* sb) {
     h8 fa[2][4], fb[2][2];
@@ -321,7 +335,7 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NJ; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[cur][j], fa[cur][i], acc[i][j], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -390,11 +404,11 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int row = wm * 128 + i * 32 + (lane & 31);
-        const int col = wn * 64 + j * 32 + g * 8 + (lane >> 5) * 4;
+        const int col = wn * 32 * NJ + j * 32 + g * 8 + (lane >> 5) * 4;
         _Float16 h[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -527,8 +541,14 @@ __global__ void __launch_bounds__(T4, 1)
   int e = 0, m0 = 0, m_end = 0;
   if (!grouped_tile(offsets, experts, R, mt, e, m0, m_end)) return;  // beyond the last tile: uniform
   const int64_t wstride = (int64_t)K * (N / 2), sstride = (int64_t)(K / group) * N, zstride = (int64_t)(K / group) * (N / 2);
-  prefill_tile<A_DIRECT, EPI_PLAIN>(lds, A, W + e * wstride, S + e * sstride, Z + e * zstride, Y, R, m0, m_end,
-                                    nt * BN, N, K, group);
+  // A last column tile of at most 128 columns (N = 1408 is 5.5 tiles) takes
+  // the narrow form: half the MFMAs and half the dequantisation per thread.
+  if (N - nt * BN <= BN / 2)
+    prefill_tile<A_DIRECT, EPI_PLAIN, true>(lds, A, W + e * wstride, S + e * sstride, Z + e * zstride, Y, R, m0,
+                                            m_end, nt * BN, N, K, group);
+  else
+    prefill_tile<A_DIRECT, EPI_PLAIN>(lds, A, W + e * wstride, S + e * sstride, Z + e * zstride, Y, R, m0, m_end,
+                                      nt * BN, N, K, group);
 }
 
 // MoE gate/up projection: rows of the pair space (sorted by expert, offsets[e]
