@@ -170,12 +170,13 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
                                              const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int a_rows,
                                              int m0, int m_end, int n0, int N, int K, int group,
                                              const RowMap rm = RowMap{}) {
-  static_assert(!NW || EPI != EPI_SILU_MUL, "prefill_tile: narrow tiles use the plain column mapping");
   // NW (narrow): the tile's columns are n0 .. n0 + 127 (a last tile of at most
-  // 128 columns); each wavefront owns 32 of them (one B fragment instead of
-  // two) and each thread dequantises 2 rows x 8 columns instead of 4 x 8.
+  // 128 columns; with EPI_SILU_MUL, 64 gate and 64 up columns); each wavefront
+  // owns 32 of them (one B fragment instead of two) and each thread
+  // dequantises 2 rows x 8 columns instead of 4 x 8.
   constexpr int NJ = NW ? 1 : 2;    // 32-column B fragments per wavefront
   constexpr int RPT = NW ? 2 : 4;   // W rows per dequantising thread
+  constexpr int HG = NW ? 8 : 16;   // EPI_SILU_MUL: column groups of 8 per gate / up half
   _Float16* const lds_a = lds;
   _Float16* const lds_b = lds + A_STAGES * A_STAGE;
   const Tile tile{m0, n0};
@@ -230,8 +231,8 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
   int n = tile.n0 + cg * 8;
   bool n_ok = n < N;
   if (EPI == EPI_SILU_MUL) {
-    const int half_cols = N / 2, a0 = tile.n0 / 2 + (cg & 15) * 8;  // activation column of this group
-    n = (cg < 16 ? 0 : half_cols) + a0;
+    const int half_cols = N / 2, a0 = tile.n0 / 2 + (cg & (HG - 1)) * 8;  // activation column of this group
+    n = (cg < HG ? 0 : half_cols) + a0;
     n_ok = a0 < half_cols;
   }
   const uint32_t w_row = (uint32_t)(N / 2);
@@ -421,15 +422,16 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
   __syncthreads();
   const int rows = min(BM, M - tile.m0);
   if (EPI == EPI_SILU_MUL) {
-    // 128 activation columns per tile: gate in staged columns 0..127, up in 128..255
+    // 128 activation columns per tile (64 when narrow): gate in staged columns
+    // 0 .. 8 HG - 1, up in 8 HG .. 16 HG - 1
     const int half_cols = N / 2, a0 = tile.n0 / 2;
-    const int acols = min(BN / 2, half_cols - a0);
+    const int acols = min(8 * HG, half_cols - a0);
 #pragma unroll 4
     for (int idx = t; idx < BM * (BN / 16); idx += T4) {
       const int row = idx >> 4, ch = idx & 15;
       if (row < rows && ch * 8 < acols) {
         const u32x4 gv = *reinterpret_cast<const u32x4*>(ct + row * C_STRIDE + ch * 8);
-        const u32x4 uv = *reinterpret_cast<const u32x4*>(ct + row * C_STRIDE + BN / 2 + ch * 8);
+        const u32x4 uv = *reinterpret_cast<const u32x4*>(ct + row * C_STRIDE + 8 * HG + ch * 8);
         u32x4 o;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -571,8 +573,13 @@ __global__ void __launch_bounds__(T4, 1)
   rm.ids = ids;
   rm.topk = topk;
   rm.pairs = pairs;
-  prefill_tile<A_GATHER, EPI_SILU_MUL>(lds, X, W + e * wstride, S + e * sstride, Z + e * zstride, act, tokens, m0,
-                                       m_end, nt * BN, N, K, group, rm);
+  // a last tile of at most 64 activation columns (I = 704 is 5.5 tiles) takes the narrow form
+  if (I - nt * (BN / 2) <= BN / 4)
+    prefill_tile<A_GATHER, EPI_SILU_MUL, true>(lds, X, W + e * wstride, S + e * sstride, Z + e * zstride, act, tokens,
+                                               m0, m_end, nt * BN, N, K, group, rm);
+  else
+    prefill_tile<A_GATHER, EPI_SILU_MUL>(lds, X, W + e * wstride, S + e * sstride, Z + e * zstride, act, tokens, m0,
+                                         m_end, nt * BN, N, K, group, rm);
 }
 
 // MoE down projection: sorted activation rows times expert e's W2 [I, H]; row m
