@@ -239,10 +239,14 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
   const uint32_t w_off = n_ok ? (uint32_t)(kq * RPT) * w_row + (uint32_t)(n / 2) : OOB;
   const uint32_t s_off = n_ok ? (uint32_t)n * 2u : OOB;
   const uint32_t z_off = n_ok ? (uint32_t)(n / 2) : OOB;
-  int b_st[8];
+  // W^T write addresses in bytes from the LDS base (stage 0); stage 1 adds a
+  // constant that fits the LDS instructions' offset field, so a write takes no
+  // address arithmetic once the stage is a compile-time constant.
+  uint32_t b_st[8];
 #pragma unroll
   for (int c = 0; c < 8; ++c)
-    b_st[c] = NW ? swz2(cg * 8 + c, kq >> 2) + (kq & 3) * 2 : swz2(cg * 8 + c, kq >> 1) + (kq & 1) * 4;
+    b_st[c] = (uint32_t)(A_STAGES * A_STAGE +
+                         (NW ? swz2(cg * 8 + c, kq >> 2) + (kq & 3) * 2 : swz2(cg * 8 + c, kq >> 1) + (kq & 1) * 4)) * 2u;
 
   // fragment read offsets (halfs) for k16 step ks and row parity of the fragment index
   const int fa_base = (wm * 128 + (lane & 31)) * 64;
@@ -277,7 +281,8 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
     r.s = __builtin_amdgcn_raw_buffer_load_b128(rs, s_off, g * (uint32_t)N * 2u, 0);
     r.z = __builtin_amdgcn_raw_buffer_load_b32(rz, z_off, g * w_row, 0);
   };
-  auto dequant_store = [&](const WRegs4& r, _Float16* st) {
+  auto dequant_store = [&](const WRegs4& r, auto stage) {
+    char* const st = reinterpret_cast<char*>(lds) + decltype(stage)::value * B_STAGE * 2;
     f16x2 zh[4], sh[4];
     unpack8x(r.z, zh);
     scales_x(r.s, sh);
@@ -350,7 +355,7 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
   issue_w(wr, 0);
   __builtin_amdgcn_s_waitcnt(WAIT_VM0);
   if (EPI == EPI_SCALE_SCATTER && (unsigned)pf_pid < (unsigned)rm.pairs) pf_w = rm.w[pf_pid];
-  dequant_store(wr, lds_b);
+  dequant_store(wr, std::integral_constant<int, 0>{});
   if (nk > 1) issue_w(wr, 1);
   __syncthreads();
 
@@ -358,32 +363,42 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
   // earlier); then issue A(kt + 2) and W(kt + 2).  Consuming the registers
   // before re-issuing into them keeps one W register set, and the wait before
   // the dequantisation only covers loads issued a full step earlier.
-  auto dequant_and_issue = [&](int kt) {
+  // The W^T stage alternates with kt; the loop below is unrolled by two so that
+  // it is a constant (SB = kt & 1) in each copy.
+  auto dequant_and_issue = [&](int kt, auto next_stage) {
     if (kt + 1 < nk) {
       __builtin_amdgcn_s_waitcnt(WAIT_VM0);
-      dequant_store(wr, lds_b + ((kt + 1) & 1) * B_STAGE);
+      dequant_store(wr, next_stage);
     }
     if (kt + 2 < nk) {
       issue_a(kt + 2);
       issue_w(wr, kt + 2);
     }
   };
-  for (int kt = 0; kt < nk; ++kt) {
+  auto step = [&](int kt, auto sbc) {
+    constexpr int SB = decltype(sbc)::value;
+    const std::integral_constant<int, SB ^ 1> next{};
     if (wm == 1) {
-      dequant_and_issue(kt);
+      dequant_and_issue(kt, next);
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_s_setprio(1);
-      mfma_stage(lds_a + (kt % A_STAGES) * A_STAGE, lds_b + (kt & 1) * B_STAGE);
+      mfma_stage(lds_a + (kt % A_STAGES) * A_STAGE, lds_b + SB * B_STAGE);
       __builtin_amdgcn_s_setprio(0);
     } else {
       __builtin_amdgcn_s_setprio(1);
-      mfma_stage(lds_a + (kt % A_STAGES) * A_STAGE, lds_b + (kt & 1) * B_STAGE);
+      mfma_stage(lds_a + (kt % A_STAGES) * A_STAGE, lds_b + SB * B_STAGE);
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_s_barrier();
-      dequant_and_issue(kt);
+      dequant_and_issue(kt, next);
     }
     __syncthreads();
+  };
+  int kt = 0;
+  for (; kt + 1 < nk; kt += 2) {
+    step(kt, std::integral_constant<int, 0>{});
+    step(kt + 1, std::integral_constant<int, 1>{});
   }
+  if (kt < nk) step(kt, std::integral_constant<int, 0>{});
 
   // Epilogue: stage the fp16 tile in LDS, then store 16-byte row chunks.
   // Accumulator elements 4g .. 4g+3 of fragment (i, j) are row i*32 + lane%32,
