@@ -55,17 +55,21 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int GROUP_M = 4;  // tile rows per ordering group
 
-// (1024 + q) half2 pairs of one packed dword in the order columns (0,2), (4,6),
-// (1,3), (5,7): one byte permute per pair takes two codes from the masked
-// nibble word and the 0x64 high bytes from a constant word, so no OR is needed.
+// Code half2 pairs of one packed dword in the order columns (0,2), (4,6),
+// (1,3), (5,7): one byte permute per pair takes two code bytes from the masked
+// word and the high bytes from a constant word, so no OR is needed.  Even
+// columns (low nibbles) sit under 0x64 and read 1024 + q; odd columns keep
+// their nibble in bits 7:4 and sit under 0x54, whose mantissa unit is 1/16, so
+// they read 64 + q with no shift.  Zero-points unpacked the same way give
+// exact (1024 + q) - (1024 + z) and (64 + q) - (64 + z) = q - z.
 __device__ __forceinline__ void unpack8x(uint32_t w, f16x2 (&h)[4]) {
-  const uint32_t even = w & 0x0F0F0F0Fu;         // columns 0, 2, 4, 6
-  const uint32_t odd = (w >> 4) & 0x0F0F0F0Fu;   // columns 1, 3, 5, 7
-  const uint32_t c64 = 0x64646464u;
+  const uint32_t even = w & 0x0F0F0F0Fu;  // columns 0, 2, 4, 6
+  const uint32_t odd = w & 0xF0F0F0F0u;   // columns 1, 3, 5, 7, nibbles in bits 7:4
+  const uint32_t c64 = 0x64646464u, c54 = 0x54545454u;
   h[0] = as_h2(perm(c64, even, 0x04010400u));
   h[1] = as_h2(perm(c64, even, 0x04030402u));
-  h[2] = as_h2(perm(c64, odd, 0x04010400u));
-  h[3] = as_h2(perm(c64, odd, 0x04030402u));
+  h[2] = as_h2(perm(c54, odd, 0x04010400u));
+  h[3] = as_h2(perm(c54, odd, 0x04030402u));
 }
 // Scale half2 pairs (0,1), (2,3), (4,5), (6,7) reordered to unpack8x's order.
 __device__ __forceinline__ void scales_x(const u32x4 s, f16x2 (&h)[4]) {
