@@ -638,11 +638,12 @@ __global__ void __launch_bounds__(T4, 1)
 // a row, column or unit does not exist, so no load sits behind a branch and
 // the compiler's wait before a unit covers only that unit.  The MFMAs
 // (v_mfma_f32_16x16x32_f16, A rows >= M zero; fragment f holds columns
-// 16c + f, c = lane % 16) take the codes themselves as 1024 + q, built from
-// the packed bytes by one byte permute per two rows and an and-or per nibble
-// (about one VALU instruction per weight, against 2.4 for dequantising each
-// weight first); the scale and zero-point enter once per group, in fp32:
-// sum_k a (q - z) s = s (sum_k a (1024 + q) - (1024 + z) sum_k a), with the A
+// 16c + f, c = lane % 16) take the codes themselves as c0 + q (c0 = 1024 for
+// even columns, 64 for odd ones), built from the packed bytes by one byte
+// permute per two rows and an and-or per nibble (under one VALU instruction
+// per weight, against 2.4 for dequantising each weight first); the scale and
+// zero-point enter once per group, in fp32:
+// sum_k a (q - z) s = s (sum_k a (c0 + q) - (c0 + z) sum_k a), with the A
 // row sums from one more MFMA against ones.  The weights are therefore not
 // rounded to fp16 before the product (the dense and grouped kernels round
 // them, as the reference dequantisation does); the difference stays far below
@@ -737,10 +738,12 @@ __global__ void __launch_bounds__(DEC_THREADS)
     d.z1 = __builtin_amdgcn_raw_buffer_load_b32(rz, z_off1, kz, 0);
   };
   // One unit's MFMAs on the raw codes: B fragment f holds column 16c + f as
-  // 1024 + q (exact in fp16) for the lane's 8 rows, built straight from the
+  // c0 + q (exact in fp16) for the lane's 8 rows, built straight from the
   // packed bytes: one byte permute takes byte b of rows 2i and 2i+1, and an
-  // and-or (after a 4-bit shift for the odd column) places the two nibbles
-  // under the 0x6400 exponent, so each half2 is a k-pair of one column.  The
+  // and-or places the two nibbles of a column under an fp16 exponent, so each
+  // half2 is a k-pair of one column.  Even columns (bits 3:0) go under 0x64
+  // and read 1024 + q; odd columns stay in bits 7:4 under 0x54, whose mantissa
+  // unit is 1/16, and read 64 + q with no shift.  The
   // scale and zero-point are applied once per group to the fp32 sums (fold
   // below); a ninth-row MFMA against ones accumulates the A row sums it needs.
   const h8 ones = __builtin_bit_cast(h8, u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u});
@@ -758,8 +761,8 @@ __global__ void __launch_bounds__(DEC_THREADS)
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
           const uint32_t pb = perm(y, x, (uint32_t)b | 0x0C00u | ((uint32_t)(4 + b) << 16) | 0x0C000000u);
-          col[2 * b][i] = (pb & 0x000F000Fu) | 0x64006400u;
-          col[2 * b + 1][i] = ((pb >> 4) & 0x000F000Fu) | 0x64006400u;
+          col[2 * b][i] = (pb & 0x000F000Fu) | 0x64006400u;      // even column: 1024 + q
+          col[2 * b + 1][i] = (pb & 0x00F000F0u) | 0x54005400u;  // odd column: 64 + q (unit 1/16)
         }
       }
 #pragma unroll
@@ -770,14 +773,15 @@ __global__ void __launch_bounds__(DEC_THREADS)
       }
     }
   };
-  // Fold of one group: sum_k a (q - z) s = s (sum_k a (1024 + q) - (1024 + z) sum_k a),
-  // in fp32, for the rows e < M only (rows past M are never stored).
+  // Fold of one group: sum_k a (q - z) s = s (sum_k a (c0 + q) - (c0 + z) sum_k a),
+  // c0 = 1024 for even columns f and 64 for odd ones, in fp32, for the rows
+  // e < M only (rows past M are never stored).
   auto fold = [&](const f32x4d (&tmp)[16], const f32x4d& asum, const DecGroup& gp) {
 #pragma unroll
     for (int f = 0; f < 16; ++f) {
       const u32x4 sv = f < 8 ? gp.s0 : gp.s1;
       const float sf = (float)__builtin_bit_cast(_Float16, (uint16_t)(sv[(f % 8) / 2] >> (16 * (f & 1))));
-      const float zf = (float)(1024u + (((f < 8 ? gp.z0 : gp.z1) >> (4 * (f % 8))) & 15u));
+      const float zf = (float)((f & 1 ? 64u : 1024u) + (((f < 8 ? gp.z0 : gp.z1) >> (4 * (f % 8))) & 15u));
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         if (e < M) acc[f][e] = __builtin_fmaf(sf, __builtin_fmaf(-zf, asum[e], tmp[f][e]), acc[f][e]);
