@@ -176,12 +176,28 @@ def test_fp8_scale_conventions():
     per_ch = torch.rand(6, 1) + 0.5
     a = F.fp8_checkpoint_to_tb(W, per_ch)
     assert torch.equal(a.wqT, W.view(torch.uint8)) and torch.equal(a.sw, per_ch.reshape(6))
+    # weight_scale_inv is the dequantisation multiplier too (DeepSeek-V3 / FineGrainedFP8)
     b = F.fp8_checkpoint_to_tb(W, weight_scale_inv=torch.tensor(4.0))
-    assert torch.equal(b.sw, torch.full((6,), 0.25))
+    assert torch.equal(b.sw, torch.full((6,), 4.0))
     with pytest.raises(NotImplementedError, match="block"):
         F.fp8_checkpoint_to_tb(W, torch.ones(1, 1, 2))
     with pytest.raises(ValueError):
         F.fp8_checkpoint_to_tb(W)
+
+
+def test_fp8_scale_inv_round_trip():
+    """Quantise the way transformers' FineGrainedFP8 does (per output channel:
+    q = w * 448 / amax, stored scale_inv = amax / 448) and dequantise through
+    the converter's sw: the weight comes back to within e4m3's half step."""
+    w = torch.randn(8, 64, generator=torch.Generator().manual_seed(5)) * 0.02
+    amax = w.abs().amax(dim=1, keepdim=True)
+    q = (w * (448.0 / amax)).to(torch.float8_e4m3fn)
+    inv = amax / 448.0
+    f = F.fp8_checkpoint_to_tb(q, weight_scale_inv=inv)
+    back = f.wqT.view(torch.float8_e4m3fn).to(torch.float32) * f.sw[:, None]
+    # e4m3 keeps 3 mantissa bits: relative error at most 2^-4 of each value
+    assert torch.all((back - w).abs() <= w.abs() * 2.0 ** -4 + 1e-12)
+    assert torch.allclose(back, w, rtol=0.07, atol=1e-4)
 
 
 def test_safetensors_round_trip(tmp_path):

@@ -324,6 +324,46 @@ def test_w4a16_decode_alternating_inputs(gpu, M):
         assert torch.equal(outs[i], outs[i % 2]), f"call {i} differs from call {i % 2}"
 
 
+def test_w4a16_decode_graph_survives_workspace_growth(gpu):
+    """A graph captured at M = 1 keeps the workspace address it was captured
+    with; a later eager M = 16 call needs a larger workspace.  The old buffer
+    must stay alive and zeroed, so every replay (with eager calls between the
+    replays) still matches the oracle."""
+    from tilebench_amd import runtime as rt
+    from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip
+
+    _say("w4a16_gemm decode graph + workspace growth")
+    key = str(gpu)
+    if key in rt._workspaces:  # start from no cached workspace; the old one stays alive
+        rt._retired.append(rt._workspaces.pop(key))
+    K, N, G = 4096, 11008, 128
+    small = T.generate_w4a16_gemm_inputs(1, K, N, G, seed=31, device="cpu")
+    big = T.generate_w4a16_gemm_inputs(16, K, N, G, seed=32, device="cpu")
+    refs = [oracle.w4a16_gemm(A.numpy(), p.numpy(), s.numpy(), z.numpy(), G) for A, p, s, z, G in (small, big)]
+    d_small = tuple(t.to(gpu) if isinstance(t, torch.Tensor) else t for t in small)
+    d_big = tuple(t.to(gpu) if isinstance(t, torch.Tensor) else t for t in big)
+    impl_hip.run(*d_small)  # allocates the (small) workspace eagerly
+    torch.cuda.synchronize()
+    ws_small = rt._workspaces[key].data_ptr()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y_graph = impl_hip.run(*d_small)
+    y_big = impl_hip.run(*d_big)  # grows the workspace: a new buffer becomes the cached one
+    torch.cuda.synchronize()
+    assert rt._workspaces[key].data_ptr() != ws_small, "M = 16 should have needed a larger workspace"
+    assert any(b.data_ptr() == ws_small for b in rt._retired), "the captured workspace was released"
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(y_graph.cpu().numpy().astype(np.float32), refs[0].astype(np.float32),
+                                   atol=1e-2, rtol=1e-2, err_msg=f"replay {i}")
+        y_big = impl_hip.run(*d_big)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(y_big.cpu().numpy().astype(np.float32), refs[1].astype(np.float32),
+                                   atol=1e-2, rtol=1e-2, err_msg=f"eager call after replay {i}")
+    del graph
+
+
 # ----------------------------------------------------------------------------- fp8 GEMM
 
 def _fp8_gemm_check(gpu, M, N, K, seed):
@@ -522,7 +562,7 @@ def test_matmul_int8_bit_exact(gpu, M, N, K):
     assert splits == {(2048, 2048, 20480): 4, (600, 520, 4736): 4, (256, 512, 16384): 8}.get((M, N, K), 1)
 
 
-@pytest.mark.parametrize("M,N,K", [(512, 512, 1024), (300, 136, 256), (4096, 4096, 4096)])
+@pytest.mark.parametrize("M,N,K", [(512, 512, 1024), (300, 136, 256), (4096, 4096, 4096), (4096, 4096, 20480)])
 def test_matmul_fp16(gpu, M, N, K):
     from tilebench_amd.benchmarks.operators.matmul_fp32_fp16_fp8 import impl_hip
 
@@ -535,7 +575,7 @@ def test_matmul_fp16(gpu, M, N, K):
     np.testing.assert_allclose(out.cpu().numpy()[rows].astype(np.float32), ref, atol=2e-3, rtol=2e-3)
 
 
-@pytest.mark.parametrize("M,N,K", [(512, 512, 1024), (300, 136, 64), (4096, 4096, 2048)])
+@pytest.mark.parametrize("M,N,K", [(512, 512, 1024), (300, 136, 64), (4096, 4096, 2048), (4096, 4096, 20480)])
 def test_matmul_fp32_three_bf16_products(gpu, M, N, K):
     """fp32 operands through hi/lo bf16 splits: within 1e-4 of the float64 product,
     an order of magnitude tighter than TF32 (10 mantissa bits) would allow."""
@@ -550,7 +590,7 @@ def test_matmul_fp32_three_bf16_products(gpu, M, N, K):
     np.testing.assert_allclose(out.cpu().numpy()[rows], ref, atol=1e-4, rtol=1e-4)
 
 
-@pytest.mark.parametrize("M,N,K", [(512, 512, 1024), (300, 136, 128), (4096, 4096, 4096)])
+@pytest.mark.parametrize("M,N,K", [(512, 512, 1024), (300, 136, 128), (4096, 4096, 4096), (4096, 4096, 20480)])
 def test_matmul_fp8(gpu, M, N, K):
     """e4m3(bf16(a @ b)): fp32 accumulation against the oracle's float64 may move a
     bf16 rounding on rare values, so codes agree exactly on > 99.5 % and the

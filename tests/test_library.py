@@ -70,6 +70,23 @@ def test_w4a16_workspace_contract(lib):
     assert "workspace" in lib.tb_last_error().decode()
 
 
+def test_w4a16_refuses_operands_past_2gib(lib):
+    """Buffer offsets are 32-bit with a 2^31 out-of-range sentinel: an A, W or
+    scale operand of 2 GiB or more is refused before any launch."""
+    fake = 1 << 40
+    # prefill with M * K * 2 = 2^31 bytes of A
+    assert lib.tb_w4a16_gemm(fake, fake, fake, fake, fake, 1 << 18, 11008, 4096, 128, None, 0, None) \
+        == rt.TB_E_INVALID
+    assert "2 GiB" in lib.tb_last_error().decode()
+    # W of K * N / 2 = 2^31 bytes (decode shape)
+    assert lib.tb_w4a16_gemm(fake, fake, fake, fake, fake, 1, 1 << 16, 1 << 16, 128, None, 0, None) \
+        == rt.TB_E_INVALID
+    assert "2 GiB" in lib.tb_last_error().decode()
+    # just below the limit the shape checks pass and the missing workspace is what fails
+    assert lib.tb_w4a16_gemm(fake, fake, fake, fake, fake, 16, 11008, 4096, 128, None, 0, None) == rt.TB_E_INVALID
+    assert "workspace" in lib.tb_last_error().decode()
+
+
 def test_no_device_means_loud_failure():
     import torch
 

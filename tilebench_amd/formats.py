@@ -25,7 +25,9 @@ reference (Tilebench has no quantized checkpoints); their conventions are:
   stored as is; ``scales`` fp16 [K/G, N].
 * fp8 (e4m3) checkpoints: ``weight`` [N, K] (already K-contiguous, i.e. WqT),
   ``weight_scale`` per tensor (a scalar) or per output channel ([N] or
-  [N, 1]); some store the reciprocal (``weight_scale_inv``).  MI300-era
+  [N, 1]); DeepSeek-V3-style checkpoints name it ``weight_scale_inv`` (the
+  inverse of the quantisation factor, so again the dequantisation
+  multiplier: W ~= Wq * weight_scale_inv).  MI300-era
   checkpoints use e4m3fnuz (exponent bias 8, NaN 0x80, max 240); those codes
   are re-encoded as e4m3fn by value: every fnuz value that is a multiple of
   2^-9 is an fn value, and the eight magnitudes that are odd multiples of
@@ -208,8 +210,14 @@ def _fnuz_to_fn_codes(codes: torch.Tensor) -> torch.Tensor:
 def fp8_checkpoint_to_tb(weight: torch.Tensor, weight_scale: torch.Tensor | float | None = None, *,
                          weight_scale_inv: torch.Tensor | float | None = None) -> Fp8Weights:
     """An fp8 linear layer (weight [N, K] in e4m3fn or e4m3fnuz, or its uint8
-    codes as e4m3fn) with a per-tensor or per-output-channel scale (or its
-    reciprocal) -> WqT codes [N, K] and sw fp32 [N]."""
+    codes as e4m3fn) with a per-tensor or per-output-channel scale -> WqT codes
+    [N, K] and sw fp32 [N].
+
+    Both checkpoint keys hold the dequantisation multiplier, W ~= Wq * scale:
+    `weight_scale` (compressed-tensors / vLLM fp8 layers) and
+    `weight_scale_inv` (DeepSeek-V3 and transformers' FineGrainedFP8, where the
+    name says it is the inverse of the quantisation factor 448 / amax, i.e.
+    amax / 448).  Either one is therefore sw as it stands."""
     if (weight_scale is None) == (weight_scale_inv is None):
         raise ValueError("give exactly one of weight_scale and weight_scale_inv")
     N, K = weight.shape
@@ -228,8 +236,6 @@ def fp8_checkpoint_to_tb(weight: torch.Tensor, weight_scale: torch.Tensor | floa
     else:
         raise NotImplementedError(f"fp8 scale of shape {tuple(s.shape)} for a [{N}, {K}] weight: only per-tensor "
                                   f"and per-output-channel scales fit the row/column-scaled GEMM (block scales do not)")
-    if weight_scale_inv is not None:
-        s = 1.0 / s
     return Fp8Weights(codes.contiguous(), s.contiguous().to(torch.float32))
 
 

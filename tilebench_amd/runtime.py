@@ -54,6 +54,7 @@ SIGNATURES: dict[str, list] = {
     "tb_matmul_workspace_size": [_c_int, _c_i64, _c_i64, _c_i64, ctypes.POINTER(_c_i64)],
     "tb_l2_flush": [_c_p, _c_i64, _c_u32, _c_p],
     "tb_probe_copy": [_c_p, _c_p, _c_i64, _c_p],
+    "tb_probe_read": [_c_p, _c_i64, _c_u32, _c_p, _c_p],
     "tb_probe_mfma": [_c_int, _c_i64, _c_i64, _c_p, _c_p],
 }
 
@@ -141,6 +142,8 @@ def ptr(t) -> int:
 
 
 _workspaces: dict = {}
+#: every workspace ever handed out, kept alive until the process ends
+_retired: list = []
 
 
 def matmul_workspace_size(dtype: int, M: int, N: int, K: int) -> int:
@@ -159,7 +162,12 @@ def workspace(nbytes: int, device, stream: int):
     capture: the engine and the bench always run a call eagerly first).  One
     buffer per device serves calls issued in order on one stream (graph
     replays included); calls running concurrently on several streams of one
-    device would race on it and are not supported."""
+    device would race on it and are not supported.
+
+    When a call needs more than the cached buffer holds, a larger one becomes
+    the cached buffer and the old one is kept alive (never returned to the
+    caching allocator): a graph captured earlier holds the old buffer's raw
+    address, and its replays must keep finding a live, zeroed workspace there."""
     import torch
 
     del stream  # calls are serialised on one stream; see the docstring
@@ -170,6 +178,8 @@ def workspace(nbytes: int, device, stream: int):
     if buf is None or buf.numel() < nbytes:
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError("workspace must be allocated before graph capture (run the op once eagerly)")
-        buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _workspaces[key] = buf
+        new = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        if buf is not None:
+            _retired.append(buf)
+        _workspaces[key] = buf = new
     return buf
