@@ -100,7 +100,7 @@ def test_a_missing_launch_fails_even_when_every_name_is_right(tmp_path):
     g = _counters(tmp_path / "c.csv", PIPELINE[:3])
     v = cp.validate_capture([f, g], PIPELINE)
     assert not v["ok"]
-    assert any("c.csv" in p and "captured 3 != expected 4" in p for p in v["problems"])
+    assert any("c.csv" in p and "dispatch count 3, manifest expects 4" in p for p in v["problems"])
 
 
 @pytest.mark.parametrize("intruder", ["__amd_rocclr_copyBuffer", "at::native::vectorized_elementwise_kernel<4>"])
@@ -113,19 +113,19 @@ def test_a_non_operator_kernel_in_the_capture_fails(tmp_path, intruder):
 def test_launch_order_is_checked(tmp_path):
     f = _trace(tmp_path / "t.csv", [PIPELINE[1], PIPELINE[0]] + PIPELINE[2:])
     v = cp.validate_capture(f, PIPELINE)
-    assert not v["ok"] and any("order differs at launch 0" in p for p in v["problems"])
+    assert not v["ok"] and any("out-of-order dispatch #0" in p for p in v["problems"])
 
 
 def test_an_unexpected_backend_kernel_fails(tmp_path):
     other = ["tb::ntg::unpack_i2_tile", "tb::ntg::nt_gemm<3, 4, 256, 256, 128, 64>"] * 2
     v = cp.validate_capture(_trace(tmp_path / "t.csv", other), PIPELINE)
-    assert not v["ok"] and any("unexpected kernels" in p for p in v["problems"])
+    assert not v["ok"] and any("outside the manifest" in p for p in v["problems"])
 
 
 def test_an_empty_or_absent_capture_fails(tmp_path):
-    assert cp.sequence_problems(PIPELINE, []) == ["nothing captured"]
+    assert cp.sequence_problems(PIPELINE, []) == ["empty capture: no kernel dispatch recorded"]
     v = cp.validate_capture(_trace(tmp_path / "t.csv", []), PIPELINE)
-    assert not v["ok"] and any("nothing captured" in p for p in v["problems"])
+    assert not v["ok"] and any("empty capture" in p for p in v["problems"])
     v = cp.validate_capture(tmp_path / "absent.csv", PIPELINE)
     assert not v["ok"] and any("missing" in p for p in v["problems"])
     assert not cp.validate_capture([], PIPELINE)["ok"]

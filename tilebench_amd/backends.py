@@ -1,45 +1,66 @@
-"""Backend selection, shared by every entry point.
+"""The backend registry: which implementation modules exist, in which order
+results list them, and how a ``--tile-language`` selection is read.
 
-Same contract as tilebench/backends.py:13-47 (canonical order, ``--tile-language``
-parsing, file-name tag) with the MI355X backend ``hip`` appended.  torch is the
-implicit baseline and is never part of a selection.  This package ships only
-the ``hip`` implementations; the other names stay valid so that a selection
-written for the reference parses the same way (their modules are simply absent
-here and the engine skips them at import, as the reference does for a missing
-DSL, tilebench/core/engine.py:135-139).
+Interface kept from tilebench/backends.py:13-47 so that a selection, a CSV
+column order or a result file name means the same thing on both sides:
+``BACKEND_ORDER``, ``GPU_BACKENDS``, ``MODES``, ``canonical_backends``,
+``parse_backends`` and ``backend_tag``.  The registry below is one table; the
+tuples and the parser are derived from it.  ``hip`` (this package's MI355X
+kernels) is the last entry.  torch is the baseline every case runs anyway, so it
+is accepted in a selection and dropped from it.  This package ships ``impl_hip``
+modules only; the other names still parse, and the engine skips a backend whose
+module is absent (tilebench/core/engine.py:135-139 does the same for a missing
+DSL).
 """
 from __future__ import annotations
 
-#: Canonical order: drives CSV column order and the backend tag in file names.
-BACKEND_ORDER = ("triton", "cutile", "tilelang", "nki", "hip")
+from typing import Iterable, NamedTuple
 
-#: Backends measured on the GPU itself: the default selection, and what ``all`` means.
-GPU_BACKENDS = ("triton", "cutile", "tilelang", "hip")
 
-#: Run modes, as they appear in result file names.
+class _Entry(NamedTuple):
+    name: str
+    on_gpu: bool   # measured on the GPU: part of the default selection
+
+
+_REGISTRY = (
+    _Entry("triton", True),
+    _Entry("cutile", True),
+    _Entry("tilelang", True),
+    _Entry("nki", False),      # AWS Trainium: selected only by name
+    _Entry("hip", True),       # this package: hand-written gfx950 kernels
+)
+
+BACKEND_ORDER = tuple(e.name for e in _REGISTRY)
+GPU_BACKENDS = tuple(e.name for e in _REGISTRY if e.on_gpu)
 MODES = ("default", "autotune")
 
+_RANK = {name: i for i, name in enumerate(BACKEND_ORDER)}
 
-def canonical_backends(backends) -> list[str]:
-    """The selection as a duplicate-free list in canonical order."""
-    chosen = set(backends)
-    unknown = sorted(chosen - set(BACKEND_ORDER))
-    if unknown:
-        raise ValueError(f"unknown backend(s) {unknown}; choose from {', '.join(BACKEND_ORDER)}")
-    return [b for b in BACKEND_ORDER if b in chosen]
+
+def canonical_backends(backends: Iterable[str]) -> list[str]:
+    """Registry-ordered list of the named backends, each once; a name outside
+    the registry is a ValueError."""
+    names = set(backends)
+    bad = names.difference(_RANK)
+    if bad:
+        raise ValueError(f"unknown backend(s) {sorted(bad)}; choose from {', '.join(BACKEND_ORDER)}")
+    return sorted(names, key=_RANK.__getitem__)
 
 
 def parse_backends(text: str | None) -> list[str]:
-    """Parse a ``--tile-language`` value. None or ``all`` selects the GPU
-    backends; ``torch`` is accepted and ignored because it always runs."""
+    """Read a comma-separated ``--tile-language`` value (case-insensitive).
+    Missing, or containing ``all``: every GPU backend.  ``torch`` is dropped."""
     if text is None:
         return list(GPU_BACKENDS)
-    tokens = [t.strip().lower() for t in text.split(",") if t.strip()]
-    if "all" in tokens:
+    words = {w.strip().lower() for w in text.split(",")} - {""}
+    if "all" in words:
         return list(GPU_BACKENDS)
-    return canonical_backends(t for t in tokens if t != "torch")
+    words.discard("torch")
+    return canonical_backends(words)
 
 
-def backend_tag(backends) -> str:
-    """File-name tag of a selection (order-independent); ``torch`` if empty."""
-    return "-".join(canonical_backends(backends)) or "torch"
+def backend_tag(backends: Iterable[str]) -> str:
+    """Name fragment for result files: the selection joined by '-' in registry
+    order (so any typing order gives one tag), or ``torch`` when empty."""
+    chosen = canonical_backends(backends)
+    return "-".join(chosen) if chosen else "torch"

@@ -1,25 +1,39 @@
-"""Architecture of the GPU this process runs on, and its last-level cache.
+"""The GPU this process runs on: its architecture family and the cache a
+cold-entry measurement has to evict.
 
-Mirrors tilebench/hardware.py (``detect_arch:73``, ``last_level_cache_bytes:95``,
-``_LLC_BYTES:38``) with CDNA4 added: gfx950 (MI350X / MI355X) maps to "cdna4".
-Nothing touches the GPU at import time; without a GPU every probe returns None.
+Interface kept from tilebench/hardware.py (``detect_arch:73``,
+``last_level_cache_bytes:95``, the ``_LLC_BYTES:38`` table,
+``UncalibratedCacheError``, ``device_info``) because the timer and the
+verifier's per-architecture tolerance overrides key on it; the family names are
+the reference's ("cdna3", "hopper", "blackwell") plus "cdna4" for gfx950.
+
+The device is looked up once, on first use; importing this module touches no
+GPU, and on a host without one every lookup answers None.
 """
 from __future__ import annotations
 
 import functools
 from typing import NamedTuple
 
-_NVIDIA_ARCH = {(10, 0): "blackwell", (9, 0): "hopper"}
-_AMD_ARCH = {"gfx942": "cdna3", "gfx950": "cdna4"}
+MiB = 1024 * 1024
 
-#: Device-level last-level cache to evict for a cold-entry measurement, where the
-#: runtime's L2 size is not that cache.  cdna3: the reference's validated MI300X
-#: value.  cdna4 (MI355X): 8 XCDs x 4 MiB L2 in front of a 256 MiB Infinity Cache
-#: (MALL) shared by all 256 CUs; the eviction sweep that validates this entry is
-#: recorded in profiles/llc_eviction_sweep.txt.
-_LLC_BYTES: dict[str, int] = {"cdna3": 256 * 1024 * 1024, "cdna4": 256 * 1024 * 1024}
+#: gcnArchName prefix (before the first ':') -> family, for AMD devices.
+_AMD_FAMILIES = {"gfx942": "cdna3", "gfx950": "cdna4"}
+#: CUDA compute capability -> family, for NVIDIA devices.
+_NVIDIA_FAMILIES = {(9, 0): "hopper", (10, 0): "blackwell"}
 
-#: Architectures whose runtime L2 is known not to be the last-level cache.
+#: Bytes to evict for a cold-entry measurement on families whose runtime
+#: L2_cache_size is not the last-level cache.  On both CDNA families the
+#: last level is a 256 MiB Infinity Cache (MALL) behind the per-XCD L2s:
+#: cdna3 is the reference's swept MI300X value; cdna4 (MI355X) is registered
+#: at the same size, and the flush-size sweep of
+#: tilebench_amd/profiling/mall_sweep.py (profiles/mall_sweep_MI355X.txt)
+#: shows a 512 MiB flush (the timer's 2x rule) leaves a re-read probe as cold
+#: as any larger one.
+_LLC_BYTES: dict[str, int] = {"cdna3": 256 * MiB, "cdna4": 256 * MiB}
+
+#: Families whose L2 is known not to be the last level: without an entry in
+#: _LLC_BYTES a cold measurement is refused rather than silently warm.
 _LLC_CALIBRATION_REQUIRED = frozenset({"cdna3", "cdna4"})
 
 
@@ -28,49 +42,64 @@ class UncalibratedCacheError(RuntimeError):
 
 
 class DeviceInfo(NamedTuple):
-    vendor: str
+    vendor: str                          # "amd" or "nvidia"
     name: str
-    capability: tuple[int, int] | None
-    gcn_arch_name: str | None
+    capability: tuple[int, int] | None   # NVIDIA only
+    gcn_arch_name: str | None            # AMD only, e.g. "gfx950:sramecc+:xnack-"
+
+
+def _current_properties():
+    """(torch, properties of the current device), or None without a GPU."""
+    import torch
+
+    if not torch.cuda.is_available():
+        return None
+    return torch, torch.cuda.get_device_properties(torch.cuda.current_device())
 
 
 @functools.cache
 def device_info() -> DeviceInfo | None:
     try:
-        import torch
-
-        if not torch.cuda.is_available():
-            return None
-        index = torch.cuda.current_device()
-        props = torch.cuda.get_device_properties(index)
-        if torch.version.hip:
-            return DeviceInfo("amd", props.name, None, getattr(props, "gcnArchName", None) or None)
-        return DeviceInfo("nvidia", props.name, tuple(torch.cuda.get_device_capability(index)), None)
+        found = _current_properties()
     except Exception:
         return None
+    if found is None:
+        return None
+    torch, props = found
+    if torch.version.hip:
+        return DeviceInfo("amd", props.name, None, getattr(props, "gcnArchName", None) or None)
+    try:
+        cap = tuple(torch.cuda.get_device_capability(torch.cuda.current_device()))
+    except Exception:
+        return None
+    return DeviceInfo("nvidia", props.name, cap, None)
 
 
 @functools.cache
 def detect_arch() -> str | None:
-    """"cdna4" (gfx950), "cdna3" (gfx942), "blackwell", "hopper" or None."""
-    dev = device_info()
-    if dev is None:
+    """Family of the current device ("cdna4" for gfx950), or None when there
+    is no GPU or the device is outside the families above."""
+    info = device_info()
+    if info is None:
         return None
-    if dev.vendor == "nvidia":
-        return _NVIDIA_ARCH.get(dev.capability)
-    return _AMD_ARCH.get((dev.gcn_arch_name or "").split(":")[0])
+    if info.vendor == "amd":
+        base = (info.gcn_arch_name or "").partition(":")[0]
+        return _AMD_FAMILIES.get(base)
+    return _NVIDIA_FAMILIES.get(info.capability)
 
 
 def last_level_cache_bytes() -> int | None:
-    """Size of the cache a cold-entry measurement must evict, or None."""
-    arch = detect_arch()
-    if arch in _LLC_BYTES:
-        return _LLC_BYTES[arch]
-    if arch in _LLC_CALIBRATION_REQUIRED:
-        raise UncalibratedCacheError(f"{arch} LLC eviction size has not been calibrated")
+    """Bytes a flush must cover to evict the device's last-level cache, or None."""
+    family = detect_arch()
+    registered = _LLC_BYTES.get(family) if family else None
+    if registered is not None:
+        return registered
+    if family in _LLC_CALIBRATION_REQUIRED:
+        raise UncalibratedCacheError(
+            f"no validated last-level cache size for {family}: register one in "
+            f"tilebench_amd.hardware._LLC_BYTES after an eviction sweep")
     try:
-        import torch
-
-        return torch.cuda.get_device_properties(torch.cuda.current_device()).L2_cache_size
+        found = _current_properties()
     except Exception:
         return None
+    return None if found is None else found[1].L2_cache_size
