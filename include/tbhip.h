@@ -256,8 +256,9 @@ tb_status tb_matmul_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, i
 
 /*
  * Fill `bytes` bytes of `buf` with a 32-bit pattern using a plain store
- * kernel.  Used to evict the L2 and the 256 MiB MALL between timed launches
- * (a kernel, not hipMemset, so it may be captured into a graph).
+ * kernel (cache-allocating stores: nontemporal ones would leave the MALL's
+ * contents in place).  Used to evict the L2 and the 256 MiB MALL between
+ * timed launches (a kernel, not hipMemset, so it may be captured into a graph).
  * Requires bytes % 16 == 0 and a 16-byte aligned buffer.
  * Replaces: tilebench/core/timer.py:107 _flush_l2_cache().
  */
@@ -271,11 +272,23 @@ tb_status tb_l2_flush(void* buf, int64_t bytes, uint32_t pattern, hipStream_t st
 tb_status tb_probe_copy(const void* src, void* dst, int64_t bytes, hipStream_t stream);
 
 /*
+ * Eviction-sweep probe: a streaming read of `bytes` bytes of src (16-byte
+ * granules, plain cache-allocating loads).  sink[0] is written only if the
+ * XOR of a granule's four words equals `key` (pick a key the data cannot
+ * produce, so nothing is written).  The re-read probe placed behind flushes of
+ * growing size to find the last-level cache's eviction size.
+ * Replaces: the re-read probe of the reference's eviction sweep, described at
+ * tilebench/hardware.py:24-37.
+ */
+tb_status tb_probe_read(const void* src, int64_t bytes, uint32_t key, uint32_t* sink, hipStream_t stream);
+
+/*
  * Calibration probe: `blocks` x 256 threads, each wavefront issuing
  * 8 * iters independent MFMAs (kind 0: v_mfma_f32_32x32x16_f16, 32768 flop
- * each; kind 1: v_mfma_f32_32x32x64_f8f6f4 on e4m3, 131072 flop each), then
- * one float per thread into out[blocks * 256].  The measured MFMA peak is
- * taken from it.
+ * each; kind 1: v_mfma_f32_32x32x64_f8f6f4 on e4m3, 131072 flop each; kind 2:
+ * v_mfma_f32_32x32x16_bf16, 32768 flop each; kind 3: v_mfma_i32_32x32x32_i8,
+ * 65536 op each), then one float per thread into out[blocks * 256].  The
+ * instruction-level MFMA ceiling of the calibration is taken from it.
  * Replaces: tilebench/llm/v2/calibration/gpu_probes.py:225 probe_gemm().
  */
 tb_status tb_probe_mfma(int kind, int64_t blocks, int64_t iters, float* out, hipStream_t stream);

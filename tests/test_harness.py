@@ -252,3 +252,42 @@ def test_engine_missing_backend_module_is_skipped(fake_operator, capsys):
                                      bench_fn=lambda *a, **k: {"mean": 1.0})
     assert "triton import skipped" in capsys.readouterr().out
     assert res[0]["triton_err"] == "triton not available"
+
+
+# ----------------------------------------------------------------------------- timer
+
+
+def test_kernel_times_are_grouped_per_flushed_sample():
+    k = [("tb::fill_kernel(...)", 0.0, 80.0), ("tb::a", 81.0, 5.0), ("tb::b", 87.0, 2.0),
+         ("tb::fill_kernel(...)", 100.0, 80.0), ("tb::a", 181.0, 6.0), ("tb::b", 188.0, 2.0)]
+    assert timer.kernel_times_per_sample(k, 2, flushed=True) == [0.007, 0.008]
+    assert timer.kernel_times_per_sample(k, 3, flushed=True) is None          # wrong sample count
+    assert timer.kernel_times_per_sample(k[:4], 2, flushed=True) is None      # a sample without kernels
+    assert timer.kernel_times_per_sample([], 1, flushed=True) is None
+    plain = [("x", 0.0, 1.0), ("y", 2.0, 3.0), ("x", 6.0, 1.5), ("y", 8.0, 2.5)]
+    assert timer.kernel_times_per_sample(plain, 2, flushed=False) == [0.004, 0.004]
+    assert timer.kernel_times_per_sample(plain, 3, flushed=False) is None
+
+
+def test_named_grid_selects_the_reference_gating_grid(fake_operator, tmp_path, monkeypatch):
+    cfg = tmp_path / "config.yaml"
+    cfg.write_text("benchmark: {warmup: 1, repeat: 3}\nverify: {atol: 0, rtol: 0}\ncase_grid:\n  n: [4]\n"
+                   "  dtype: [fp32]\ngrids:\n  wide:\n    case_defaults: {n: 2}\n    case_grid:\n"
+                   "      n: [4, 8, 12]\n      dtype: [fp32]\n")
+    monkeypatch.setattr(engine, "operator_config", lambda op: cfg)
+    res = engine.run_benchmark_suite("fakeop", benchmark_overrides={"grid": "wide"}, enabled_backends=["hip"],
+                                     bench_fn=lambda *a, **k: {"mean": 1.0})
+    assert [r["params"]["n"] for r in res] == [4, 8, 12]
+    with pytest.raises(ValueError, match="no grid named"):
+        engine.run_benchmark_suite("fakeop", benchmark_overrides={"grid": "nope"}, enabled_backends=["hip"],
+                                   bench_fn=lambda *a, **k: {"mean": 1.0})
+
+
+def test_gating_config_carries_the_reference_grid():
+    import yaml
+    cfg = yaml.safe_load(open(operator_config("moe_topk_gating")))
+    alt = cfg["grids"]["reference"]
+    cases = T.expand_cases("moe_topk_gating", alt)
+    assert len(cases) == 60 and {c["dtype"] for c in cases} == {"fp16", "bf16", "fp32"}
+    assert {c["E"] for c in cases} == {128} and {c["k"] for c in cases} == {2}
+    assert sorted({c["M"] for c in cases}) == [1024 * i for i in range(1, 21)]

@@ -77,6 +77,16 @@ def run_benchmark_suite(operator_name, benchmark_overrides=None, enabled_backend
 
     bench_cfg = dict(config.get("benchmark", {}))
     bench_cfg.update(benchmark_overrides or {})
+    grid = bench_cfg.get("grid")
+    if grid is not None:
+        # a named alternative grid of the same operator (config "grids:" entry),
+        # e.g. the reference's own case grid beside the BASELINE one
+        alt = (config.get("grids") or {}).get(grid)
+        if alt is None:
+            raise ValueError(f"{operator_name}: no grid named {grid!r} in config.yaml (have "
+                             f"{sorted(config.get('grids') or {})})")
+        config = {k: v for k, v in config.items() if k not in ("case_grid", "case_defaults", "test_cases")}
+        config.update(alt)  # its own case_defaults / case_grid (and verify, if it sets one)
     warmup = int(bench_cfg.get("warmup", DEFAULT_WARMUP))
     repeat = int(bench_cfg.get("repeat", DEFAULT_REPEAT))
     autotune = bool(bench_cfg.get("autotune", False))

@@ -15,11 +15,15 @@ NON_GPU_BACKENDS = ("nki",)
 
 
 def load_peak_config(gpu_name: str) -> dict:
-    path = os.path.join(PEAK_PERFORMANCE_ROOT, f"{gpu_name}.json")
-    if not os.path.isfile(path):
-        return {}
-    with open(path) as f:
-        return json.load(f)
+    """Peaks of `gpu_name`: data/peak_performance/<gpu>.json if present, else the
+    calibrated file data/peak_performance/empirical/<gpu>.json (MI355X has only
+    the calibrated one: tilebench_amd.calibration writes it), else {}."""
+    for path in (os.path.join(PEAK_PERFORMANCE_ROOT, f"{gpu_name}.json"),
+                 os.path.join(PEAK_PERFORMANCE_ROOT, "empirical", f"{gpu_name}.json")):
+        if os.path.isfile(path):
+            with open(path) as f:
+                return json.load(f)
+    return {}
 
 
 def _eval_expr(expr, ctx: dict):
@@ -58,7 +62,7 @@ def compute_derived(result: dict, metrics_cfg: dict, peak_cfg: dict | None = Non
     peak_bw = peak.get("peak_bw_GBs") or metrics_cfg.get("peak_bw_GBs")
     peak_bw = float(peak_bw) if peak_bw is not None else None
     peak_mode = metrics_cfg.get("peak_tflops_key") or result.get("dtype")
-    raw = (peak.get("peak_tflops") or {}).get(peak_mode)
+    raw = {**(peak.get("peak_tops") or {}), **(peak.get("peak_tflops") or {})}.get(peak_mode)
     peak_tf = float(raw) if raw is not None else None
     torch_ms = result.get("torch_ms")
     torch_ms = float(torch_ms) if torch_ms is not None and torch_ms > 0 and not math.isnan(torch_ms) else None

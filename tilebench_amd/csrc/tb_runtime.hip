@@ -45,9 +45,14 @@ tb_status reserve_lds(const void* kernel, size_t bytes, const char* what) {
 // that covers the whole buffer: on MI355X that shape sustains 6.7 TB/s for a
 // 512 MiB copy, where grid-stride loops (2048-8192 blocks, four granules in
 // flight per thread) reach 4.7-5.1 TB/s and eight granules per thread 4.3 TB/s.
+//
+// The flush uses plain (cache-allocating) stores: nontemporal stores leave the
+// MALL's contents in place (a 64 MiB buffer read back after a 1 GiB
+// nontemporal fill is exactly as fast as without it), plain stores of 384 MiB
+// or more evict it (profiles/mall_sweep_MI355X.txt).
 __global__ void __launch_bounds__(256) fill_kernel(u32x4* __restrict__ dst, int64_t n16, uint32_t pattern) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n16) st_nt(dst + i, u32x4{pattern, pattern, pattern, pattern});
+  if (i < n16) dst[i] = u32x4{pattern, pattern, pattern, pattern};
 }
 
 // Streaming copy, one 16-byte granule per thread (see fill_kernel).
@@ -57,15 +62,33 @@ __global__ void __launch_bounds__(256) copy_kernel(const u32x4* __restrict__ src
   if (i < n16) st_nt(dst + i, ld_nt(src + i));
 }
 
+// Streaming read, one 16-byte granule per thread, plain (cache-allocating)
+// loads: the re-read probe of the eviction sweep.  The XOR of what a thread
+// read is stored only if it equals a key no input holds, so the loads stay
+// live without writing anything.
+__global__ void __launch_bounds__(256) read_kernel(const u32x4* __restrict__ src, int64_t n16, uint32_t key,
+                                                   uint32_t* __restrict__ sink) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n16) {
+    const u32x4 v = src[i];
+    const uint32_t x = v[0] ^ v[1] ^ v[2] ^ v[3];
+    if (x == key) sink[0] = x;
+  }
+}
+
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 // MFMA throughput probe: every wavefront keeps 8 independent 32x32 accumulators
 // busy for `iters` rounds, so the matrix pipe never waits on a dependency; the
 // accumulators are reduced to one store per lane so nothing is dead code.
 // kind 0: v_mfma_f32_32x32x16_f16 (32768 flop), kind 1: v_mfma_f32_32x32x64_f8f6f4
-// with e4m3 operands (131072 flop).
+// with e4m3 operands (131072 flop), kind 2: v_mfma_f32_32x32x16_bf16 (32768 flop),
+// kind 3: v_mfma_i32_32x32x32_i8 (65536 op).
 template <int KIND>
 __global__ void __launch_bounds__(256) mfma_probe_kernel(float* __restrict__ out, int iters, float seed) {
   f32x16 acc[8];
@@ -83,12 +106,41 @@ __global__ void __launch_bounds__(256) mfma_probe_kernel(float* __restrict__ out
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[i], 0, 0, 0);
     }
-  } else {
-    i32x8 a, b;
+  } else if constexpr (KIND == 2) {
+    bf8 a, b;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      a[i] = (int)(0x38383838u + lane + i);
-      b[i] = (int)(0x30303030u + lane - i);
+      a[i] = (__bf16)(seed * (lane + i));
+      b[i] = (__bf16)(seed * (lane - i));
+    }
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[i], 0, 0, 0);
+    }
+  } else if constexpr (KIND == 3) {
+    i32x16 iacc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) iacc[i] = i32x16{};
+    i32x4 a, b;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[i] = (int)(0x01020304u * (uint32_t)(lane + i + 1));
+      b[i] = (int)(0x04030201u * (uint32_t)(lane - i + 7));
+    }
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) iacc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, iacc[i], 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][e] = (float)iacc[i][e];
+  } else {
+    i32x8 a, b;  // e4m3 codes 0x30..0x37 (0.25 .. 0.4375) and 0x28..0x2F (0.0625 .. 0.109)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      a[i] = (int)(0x30303030u + (uint32_t)((lane + i) & 7));
+      b[i] = (int)(0x28282828u + (uint32_t)((lane ^ i) & 7));
     }
     for (int it = 0; it < iters; ++it) {
 #pragma unroll
@@ -127,12 +179,28 @@ tb_status tb_l2_flush(void* buf, int64_t bytes, uint32_t pattern, hipStream_t st
 tb_status tb_probe_mfma(int kind, int64_t blocks, int64_t iters, float* out, hipStream_t stream) {
   TB_CHECK_ARG(out != nullptr && blocks > 0 && blocks < (1 << 24) && iters > 0 && iters < (1 << 30),
                "tb_probe_mfma: bad arguments");
-  TB_CHECK_ARG(kind == 0 || kind == 1, "tb_probe_mfma: kind must be 0 (fp16) or 1 (fp8)");
+  TB_CHECK_ARG(kind >= 0 && kind <= 3, "tb_probe_mfma: kind must be 0 (fp16), 1 (fp8), 2 (bf16) or 3 (int8)");
+  const dim3 grid((unsigned)blocks), block(256);
   if (kind == 0)
-    hipLaunchKernelGGL(tb::mfma_probe_kernel<0>, dim3((unsigned)blocks), dim3(256), 0, stream, out, (int)iters, 1e-3f);
+    hipLaunchKernelGGL(tb::mfma_probe_kernel<0>, grid, block, 0, stream, out, (int)iters, 1e-3f);
+  else if (kind == 1)
+    hipLaunchKernelGGL(tb::mfma_probe_kernel<1>, grid, block, 0, stream, out, (int)iters, 1e-3f);
+  else if (kind == 2)
+    hipLaunchKernelGGL(tb::mfma_probe_kernel<2>, grid, block, 0, stream, out, (int)iters, 1e-3f);
   else
-    hipLaunchKernelGGL(tb::mfma_probe_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, stream, out, (int)iters, 1e-3f);
+    hipLaunchKernelGGL(tb::mfma_probe_kernel<3>, grid, block, 0, stream, out, (int)iters, 1e-3f);
   return tb::launch_status("tb_probe_mfma");
+}
+
+tb_status tb_probe_read(const void* src, int64_t bytes, uint32_t key, uint32_t* sink, hipStream_t stream) {
+  TB_CHECK_ARG(src && sink && bytes > 0 && bytes % 16 == 0, "tb_probe_read: bytes must be a positive multiple of 16");
+  TB_CHECK_ARG(bytes / 16 / 256 < (1ll << 31), "tb_probe_read: buffer too large");
+  TB_CHECK_ALIGN(src, 16, "src");
+  TB_CHECK_ALIGN(sink, 4, "sink");
+  const int64_t n16 = bytes / 16;
+  hipLaunchKernelGGL(tb::read_kernel, dim3(tb::grid_for(n16)), dim3(256), 0, stream,
+                     reinterpret_cast<const tb::u32x4*>(src), n16, key, sink);
+  return tb::launch_status("tb_probe_read");
 }
 
 tb_status tb_probe_copy(const void* src, void* dst, int64_t bytes, hipStream_t stream) {

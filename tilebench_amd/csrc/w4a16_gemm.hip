@@ -846,10 +846,21 @@ __global__ void __launch_bounds__(DEC_THREADS)
     for (int q = 0; q < CH; ++q) store_y(q, red[q]);
     return;
   }
-  // Serial split-K across the slab's blocks.  Partials are written through to
-  // the device-coherent level (sc1) and read back the same way, so the last
-  // block sees every other block's partial without a cache-wide fence (which
-  // would write back and invalidate the whole L2 of the XCD in every block).
+  // Serial split-K across the slab's blocks.  The hand-off uses the gfx950
+  // (GFX942-family) memory model's encoding of agent-scope atomics rather than
+  // cache-wide fences: every partial is stored and loaded with the sc1 cache
+  // policy, which is how an agent-scope monotonic atomic store / load is
+  // encoded (AMDGPUUsage, "Memory Model GFX942": the access is performed
+  // coherently across the XCDs' separate L2s instead of in one XCD's L2).
+  // Each wavefront waits for its own sc1 stores to be acknowledged
+  // (s_waitcnt vmcnt(0)) before the block barrier, and only then does thread 0
+  // bump the slab counter with an agent-scope atomic, so every partial of a
+  // block is at the coherence point before its arrival is counted.  The block
+  // that reads splits - 1 then loads the partials with sc1, which reads them
+  // from that same coherence point, never from a stale line of its XCD's L2.
+  // A release / acquire pair on the counter would add an L2 write-back
+  // (buffer_wbl2) to every block and an invalidate to the last one; measured
+  // on the box, that made the M = 1 decode about 4 us slower.
   const rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(partials, 0, 0x7FFFFFFF, (int)RSRC_DW3);
   auto poff = [&](int s2, int q) -> uint32_t {
     const int i = (threadIdx.x + q * DEC_THREADS) * 4;
@@ -859,7 +870,7 @@ __global__ void __launch_bounds__(DEC_THREADS)
 #pragma unroll
   for (int q = 0; q < CH; ++q)
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, red[q]), rp, poff(split, q), 0, AUX_SC1);
-  __builtin_amdgcn_s_waitcnt(0);  // partial stores acknowledged before the arrival is counted
+  __builtin_amdgcn_s_waitcnt(0);  // this wavefront's partial stores acknowledged
   __syncthreads();
   if (threadIdx.x == 0) {
     const int prev = __hip_atomic_fetch_add(&counters[slab], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -934,6 +945,11 @@ extern "C" tb_status tb_w4a16_gemm(const uint16_t* A, const uint8_t* W, const ui
   TB_CHECK_ARG(K % BK == 0 && group % BK == 0 && K % group == 0,
                "tb_w4a16_gemm: need K %% 64 == 0, group %% 64 == 0 and K %% group == 0 (K=%lld group=%lld)",
                (long long)K, (long long)group);
+  // Both kernels address A, W, scales and zeros through 32-bit buffer offsets
+  // whose out-of-range sentinel is 2^31: every operand must stay below 2 GiB.
+  TB_CHECK_ARG(M * K * 2 < (1ll << 31) && K * (N / 2) < (1ll << 31) && (K / group) * N * 2 < (1ll << 31),
+               "tb_w4a16_gemm: A, W and scales must each be smaller than 2 GiB (M=%lld N=%lld K=%lld)",
+               (long long)M, (long long)N, (long long)K);
   TB_CHECK_ALIGN(A, 16, "A");
   TB_CHECK_ALIGN(W, 4, "W");
   TB_CHECK_ALIGN(scales, 16, "scales");
@@ -953,8 +969,8 @@ extern "C" tb_status tb_w4a16_gemm(const uint16_t* A, const uint8_t* W, const ui
       }
     }
     const int64_t slabs = (N + DEC_COLS - 1) / DEC_COLS;
-    TB_CHECK_ARG(splits == 1 || slabs <= DEC_MAX_SLABS, "tb_w4a16_gemm: N=%lld is too wide for the decode kernel",
-                 (long long)N);
+    TB_CHECK_ARG(splits == 1 || (slabs <= DEC_MAX_SLABS && (int64_t)splits * M * N * 4 < (1ll << 31)),
+                 "tb_w4a16_gemm: N=%lld is too wide for the decode kernel", (long long)N);
     int* counters = reinterpret_cast<int*>(workspace);
     float* partials =
         need > 0 ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + DEC_COUNTER_BYTES) : nullptr;

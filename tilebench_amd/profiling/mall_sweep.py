@@ -1,17 +1,18 @@
-"""Checks the eviction size the timer flushes against the device's last-level cache.
+"""Eviction sweep: how large a flush the timer needs to start a launch cold.
 
-The timer evicts the cache before every timed launch by storing over a buffer of
-2x the last-level cache (tilebench_amd/hardware.py registers 256 MiB of MALL for
-cdna4, the datasheet figure; the reference's rule is tilebench/core/timer.py:81-104).
-This sweep measures where that cache ends: tb_probe_copy moves a working set of
-S bytes (S/2 read, S/2 written) back to back, so a working set that fits in the
-cache is served from it on every launch after the first ("warm"), and each size
-is also timed as single launches, each after a synchronisation, once without
-and once right after tb_l2_flush, the timer's own flush.  Single launches with
-and without the flush differ only in what the cache holds, so their gap is the
-cache's benefit and shows whether the flush evicts.  The back-to-back rate falls
-where S passes the cache size, if the cache serves a streaming copy faster than
-HBM does.
+The timer stores over a buffer of 2x the last-level cache before every timed
+launch (the reference's rule, tilebench/core/timer.py:81-104), and
+tilebench_amd/hardware.py registers that cache's size per architecture.  The
+reference validates its entry the way this sweep does
+(tilebench/hardware.py:24-37): a fixed re-read probe behind flushes of growing
+size.  The probe reads a P-byte buffer with plain loads (tb_probe_read).  For
+each flush size F, a sample is: read the buffer once (it is now as warm as the
+caches can make it), flush F bytes, then time one more read with hipEvents.
+While F is below what the caches hold, part of the buffer survives and the
+timed read is faster; from the eviction size on, the read is as slow as the
+cold reference (the first read of the buffer after a 2 GiB flush).  Two
+flushes are swept: tb_l2_flush (the timer's store kernel, nontemporal stores)
+and torch's fill_ (plain stores).
 
 Usage:  python -m tilebench_amd.profiling.mall_sweep --out profiles/mall_sweep_MI355X.txt
 """
@@ -25,51 +26,78 @@ import torch
 
 from tilebench_amd import hardware
 from tilebench_amd import runtime as rt
-from tilebench_amd.core.timer import _flush_l2_buffer_mb, flush_l2_cache
+from tilebench_amd.core.timer import _flush_l2_buffer_mb
 
 MIB = 1024 * 1024
-SIZES_MIB = (16, 32, 64, 96, 128, 160, 192, 224, 256, 288, 320, 384, 512, 768, 1024)
+PROBE_MIB = (64, 128)
+FLUSH_MIB = (0, 16, 32, 64, 96, 128, 160, 192, 224, 256, 320, 384, 512, 768, 1024)
+KEY = 0xDEADBEEF  # the probe buffer is all zeros: no granule XORs to this
 
 
-def _time_copy(src: torch.Tensor, dst: torch.Tensor, launches: int, flush: bool, samples_n: int = 1) -> float:
-    """Median over samples of the mean microseconds per tb_probe_copy launch."""
+def _read_us(probe: torch.Tensor, sink: torch.Tensor, flush, reps: int = 7) -> float:
+    """Median microseconds of one probe read placed right after `flush()`."""
     stream = rt.stream_handle()
-    nbytes = src.numel()
-    samples = []
-    for _ in range(samples_n):
-        if flush:
-            flush_l2_cache()
+    times = []
+    for _ in range(reps):
+        rt.call("tb_probe_read", probe.data_ptr(), probe.numel(), KEY, sink.data_ptr(), stream)  # warm it
+        flush()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for _ in range(launches):
-            rt.call("tb_probe_copy", src.data_ptr(), dst.data_ptr(), nbytes, stream)
+        rt.call("tb_probe_read", probe.data_ptr(), probe.numel(), KEY, sink.data_ptr(), stream)
         e1.record()
         torch.cuda.synchronize()
-        samples.append(e0.elapsed_time(e1) * 1000.0 / launches)
-    return statistics.median(samples)
+        times.append(e0.elapsed_time(e1) * 1000.0)
+    return statistics.median(times)
 
 
-def sweep(sizes_mib=SIZES_MIB) -> list[dict]:
+def sweep(probe_mib=PROBE_MIB, flush_mib=FLUSH_MIB) -> dict:
     rt.require_device()
-    rows = []
-    for s in sizes_mib:
-        buf = torch.empty(s * MIB, dtype=torch.uint8, device="cuda")
-        half = s * MIB // 2
-        src, dst = buf[:half], buf[half:]
-        for _ in range(3):
-            rt.call("tb_probe_copy", src.data_ptr(), dst.data_ptr(), half, rt.stream_handle())
-        warm = _time_copy(src, dst, 20, flush=False)
-        single = _time_copy(src, dst, 1, flush=False, samples_n=5)
-        cold = _time_copy(src, dst, 1, flush=True, samples_n=5)
-        rows.append({"working_set_mib": s, "warm_us": warm, "warm_tbs": s * MIB / warm / 1e6,
-                     "single_us": single, "single_tbs": s * MIB / single / 1e6,
-                     "cold_us": cold, "cold_tbs": s * MIB / cold / 1e6})
-        print(f"{s:5d} MiB  back-to-back {warm:8.1f} us {rows[-1]['warm_tbs']:5.2f} TB/s   "
-              f"single {single:8.1f} us {rows[-1]['single_tbs']:5.2f} TB/s   "
-              f"after flush {cold:8.1f} us {rows[-1]['cold_tbs']:5.2f} TB/s", flush=True)
-        del buf, src, dst
+    stream = rt.stream_handle()
+    big = torch.empty(max(max(flush_mib), 2048) * MIB, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(4, dtype=torch.uint32, device="cuda")
+
+    def nt_flush(nbytes):
+        return (lambda: None) if nbytes == 0 else \
+            (lambda: rt.call("tb_l2_flush", big.data_ptr(), nbytes, 0x3F800000, stream))
+
+    def fill_flush(nbytes):
+        view = big[:nbytes]
+        return (lambda: None) if nbytes == 0 else (lambda: view.fill_(0x5A))
+
+    out = {"probes": []}
+    for p in probe_mib:
+        probe = torch.zeros(p * MIB, dtype=torch.uint8, device="cuda")
+        cold_flush = nt_flush(2048 * MIB)
+        cold = _read_us(probe, sink, cold_flush)
+        rows = []
+        for f in flush_mib:
+            nt = _read_us(probe, sink, nt_flush(f * MIB))
+            pl = _read_us(probe, sink, fill_flush(f * MIB))
+            rows.append({"flush_mib": f, "nt_us": nt, "fill_us": pl})
+            print(f"probe {p:4d} MiB  flush {f:5d} MiB   after tb_l2_flush {nt:7.2f} us ({p * MIB / nt / 1e6:5.2f} TB/s)"
+                  f"   after fill_ {pl:7.2f} us ({p * MIB / pl / 1e6:5.2f} TB/s)   cold {cold:7.2f} us", flush=True)
+        out["probes"].append({"probe_mib": p, "cold_us": cold, "rows": rows})
+        del probe
         torch.cuda.empty_cache()
-    return rows
+    del big
+    torch.cuda.empty_cache()
+    return out
+
+
+def eviction_size(probe: dict, tol: float = 0.03) -> dict:
+    """Smallest flush (per flush kind) from which every larger flush leaves the
+    probe read within `tol` of the cold read; None if no flush gets there."""
+    res = {}
+    for kind in ("nt_us", "fill_us"):
+        cold = probe["cold_us"]
+        ok = [r[kind] >= cold * (1 - tol) for r in probe["rows"]]
+        first = None
+        for i in range(len(ok)):
+            if all(ok[i:]):
+                first = probe["rows"][i]["flush_mib"]
+                break
+        res[kind[:-3]] = first
+    return res
 
 
 def main(argv=None) -> int:
@@ -78,22 +106,29 @@ def main(argv=None) -> int:
     args = ap.parse_args(argv)
     arch = hardware.detect_arch()
     llc = hardware.last_level_cache_bytes()
-    print(f"arch {arch}; registered last-level cache {llc // MIB if llc else None} MiB; "
-          f"flush buffer {_flush_l2_buffer_mb()} MiB", flush=True)
-    rows = sweep()
+    head = (f"arch {arch}; registered last-level cache {llc // MIB if llc else None} MiB; "
+            f"timer flush buffer {_flush_l2_buffer_mb()} MiB")
+    print(head, flush=True)
+    res = sweep()
+    lines = [head, "",
+             "Each cell: median of 7 samples of [read the probe buffer; flush F MiB; time one read of it].",
+             "cold: the same read after a 2048 MiB flush.  Probe data all zeros (plain loads, tb_probe_read).", ""]
+    for p in res["probes"]:
+        ev = eviction_size(p)
+        lines.append(f"probe {p['probe_mib']} MiB, cold read {p['cold_us']:.2f} us "
+                     f"({p['probe_mib'] * MIB / p['cold_us'] / 1e6:.2f} TB/s); cold (within 3 %) from a flush of "
+                     f"{ev['nt']} MiB (tb_l2_flush) / {ev['fill']} MiB (fill_)")
+        lines.append("flush_MiB  after_tb_l2_flush_us  after_fill_us")
+        for r in p["rows"]:
+            lines.append(f"{r['flush_mib']:9d}  {r['nt_us']:20.2f}  {r['fill_us']:13.2f}")
+        lines.append("")
+    text = "\n".join(lines) + "\n"
+    print(text, flush=True)
     if args.out:
         with open(args.out, "w") as f:
-            f.write("# MALL size check: tb_probe_copy rate against working set (MI355X, one GPU)\n\n")
+            f.write("# Eviction sweep (MI355X): a fixed re-read probe behind flushes of growing size\n\n")
             f.write("Command:\n  python -m tilebench_amd.profiling.mall_sweep --out " + args.out + "\n\n")
-            f.write(f"arch {arch}; registered last-level cache {llc // MIB if llc else None} MiB; flush buffer "
-                    f"{_flush_l2_buffer_mb()} MiB.  Working set S = S/2 read + S/2 written per launch.\n"
-                    "back-to-back: mean of 20 launches after 3 untimed ones; single: median of 5 single\n"
-                    "launches, each after a synchronisation; flushed: the same, each right after tb_l2_flush\n"
-                    "over the flush buffer.\n\n")
-            f.write("working_set_MiB  b2b_us  b2b_TB/s  single_us  single_TB/s  flushed_us  flushed_TB/s\n")
-            for r in rows:
-                f.write(f"{r['working_set_mib']:15d} {r['warm_us']:7.1f} {r['warm_tbs']:9.2f} {r['single_us']:10.1f} "
-                        f"{r['single_tbs']:12.2f} {r['cold_us']:11.1f} {r['cold_tbs']:13.2f}\n")
+            f.write(text)
     return 0
 
 
