@@ -23,11 +23,14 @@ Two times come out of every sample:
     the L2's dirty lines visible to the host.  For a microsecond kernel that
     fixed cost is larger than the kernel, so it is reported, not used as the
     result.
-Without the activity records (profiler unavailable) ``mean`` falls back to the
+Without the activity records (profiler unavailable), or with an external
+rocprofiler tool attached to the process (rocprofv3 sets ROCP_TOOL_LIBRARIES;
+torch's activity records are then not trustworthy), ``mean`` falls back to the
 event bracket and ``time_source`` says so.
 """
 from __future__ import annotations
 
+import os
 import statistics
 from typing import Any, Callable
 
@@ -136,6 +139,11 @@ def _device_kernels(prof) -> list[tuple[str, float, float]]:
     return out
 
 
+def external_profiler_attached() -> bool:
+    """True when a rocprofiler-sdk tool (rocprofv3) runs inside this process."""
+    return bool(os.environ.get("ROCP_TOOL_LIBRARIES"))
+
+
 def report_benchmark(f: Callable[..., Any], tuple_of_args: tuple, kwargs: dict | None = None, *,
                      warmup: int = DEFAULT_WARMUP, repeat: int = DEFAULT_REPEAT, use_cuda_graph: bool = True,
                      flush_l2: bool = True, kernel_timestamps: bool = True, **_unused) -> dict:
@@ -176,7 +184,7 @@ def report_benchmark(f: Callable[..., Any], tuple_of_args: tuple, kwargs: dict |
         torch.cuda.synchronize()
 
     kernel_ms = None
-    if kernel_timestamps:
+    if kernel_timestamps and not external_profiler_attached():
         try:
             from torch.profiler import ProfilerActivity, profile
 
@@ -193,5 +201,6 @@ def report_benchmark(f: Callable[..., Any], tuple_of_args: tuple, kwargs: dict |
     samples = kernel_ms if kernel_ms is not None else events
     return {"mean": sum(samples) / n, "median": statistics.median(samples), "min": min(samples),
             "max": max(samples), "samples": samples,
-            "time_source": "kernel timestamps" if kernel_ms is not None else "hipEvents",
+            "time_source": ("kernel timestamps" if kernel_ms is not None else
+                            "hipEvents (rocprofiler tool attached)" if external_profiler_attached() else "hipEvents"),
             "event_mean": sum(events) / n, "event_samples": events, "mode": mode, "flush_mb": flush_mb}
