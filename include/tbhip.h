@@ -113,6 +113,23 @@ tb_status tb_w4a16_gemm(const uint16_t* A, const uint8_t* W, const uint16_t* sca
 tb_status tb_w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int64_t group, int64_t* bytes);
 
 /*
+ * tb_w4a16_gemm without a workspace and without any allocation: for callers
+ * that cannot allocate device memory (code under hipGraph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  Same operands, results and requirements as tb_w4a16_gemm; the
+ * M <= 16 decode keeps its split-K counters and partials in a file-scope
+ * device array of the library, 4 MiB + 16 KiB per GPU, held until the process
+ * ends (its address is looked up once per device; the first call on a device
+ * also clears the counters with a kernel on `stream`).  A shape whose decode
+ * needs more than that (only possible on devices with more than 256 CUs) is
+ * refused with TB_E_INVALID.  Every call on one GPU shares that GPU's array:
+ * calls that overlap in time on one GPU (several streams, or several host
+ * threads) race and must not be issued.  Allocates nothing, frees nothing.
+ */
+tb_status tb_w4a16_gemm_noalloc(const uint16_t* A, const uint8_t* W, const uint16_t* scales, const uint8_t* zeros,
+                                uint16_t* Y, int64_t M, int64_t N, int64_t K, int64_t group, hipStream_t stream);
+
+/*
  * Grouped MoE W4A16 GEMM: rows offsets[e] .. offsets[e+1]
  * of the expert-sorted activations A use expert e's int4 weights.
  *   A fp16 [R, K]; W uint8 [E, K, N/2]; scales fp16 [E, K/G, N];

@@ -87,6 +87,16 @@ def test_w4a16_refuses_operands_past_2gib(lib):
     assert "workspace" in lib.tb_last_error().decode()
 
 
+def test_noalloc_entry_point_checks_before_touching_a_device(lib):
+    fake = 1 << 40
+    assert lib.tb_w4a16_gemm_noalloc(None, fake, fake, fake, fake, 16, 11008, 4096, 128, None) == rt.TB_E_INVALID
+    assert "tb_w4a16_gemm_noalloc: null pointer" in lib.tb_last_error().decode()
+    assert lib.tb_w4a16_gemm_noalloc(fake, fake, fake, fake, fake, 1, 1 << 16, 1 << 16, 128, None) \
+        == rt.TB_E_INVALID
+    assert "2 GiB" in lib.tb_last_error().decode()
+    assert lib.tb_w4a16_gemm_noalloc(fake + 8, fake, fake, fake, fake, 4, 64, 64, 64, None) == rt.TB_E_ALIGN
+
+
 def test_no_device_means_loud_failure():
     import torch
 

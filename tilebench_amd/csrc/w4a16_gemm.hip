@@ -42,6 +42,7 @@
 #include "tb_common.h"
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #pragma clang fp contract(off)
@@ -934,31 +935,134 @@ extern "C" tb_status tb_w4a16_workspace_size(int64_t M, int64_t N, int64_t K, in
   return TB_OK;
 }
 
-extern "C" tb_status tb_w4a16_gemm(const uint16_t* A, const uint8_t* W, const uint16_t* scales, const uint8_t* zeros,
-                                   uint16_t* Y, int64_t M, int64_t N, int64_t K, int64_t group, void* workspace,
-                                   int64_t workspace_bytes, hipStream_t stream) {
-  using namespace tb::w4a16;
-  TB_CHECK_ARG(A && W && scales && zeros && Y, "tb_w4a16_gemm: null pointer");
-  TB_CHECK_ARG(M > 0 && N > 0 && K > 0 && group > 0, "tb_w4a16_gemm: sizes must be positive");
-  TB_CHECK_ARG(M < (1 << 30) && N < (1 << 30) && K < (1 << 30), "tb_w4a16_gemm: sizes too large");
-  TB_CHECK_ARG(N % 8 == 0, "tb_w4a16_gemm: N must be a multiple of 8 (got %lld)", (long long)N);
+namespace tb {
+namespace w4a16 {
+
+// Shape and alignment checks of the dense W4A16 GEMM, shared by both entry
+// points (`fn` names the caller in the messages).
+static tb_status check_dense_args(const char* fn, const uint16_t* A, const uint8_t* W, const uint16_t* scales,
+                                  const uint8_t* zeros, const uint16_t* Y, int64_t M, int64_t N, int64_t K,
+                                  int64_t group) {
+  TB_CHECK_ARG(A && W && scales && zeros && Y, "%s: null pointer", fn);
+  TB_CHECK_ARG(M > 0 && N > 0 && K > 0 && group > 0, "%s: sizes must be positive", fn);
+  TB_CHECK_ARG(M < (1 << 30) && N < (1 << 30) && K < (1 << 30), "%s: sizes too large", fn);
+  TB_CHECK_ARG(N % 8 == 0, "%s: N must be a multiple of 8 (got %lld)", fn, (long long)N);
   TB_CHECK_ARG(K % BK == 0 && group % BK == 0 && K % group == 0,
-               "tb_w4a16_gemm: need K %% 64 == 0, group %% 64 == 0 and K %% group == 0 (K=%lld group=%lld)",
-               (long long)K, (long long)group);
+               "%s: need K %% 64 == 0, group %% 64 == 0 and K %% group == 0 (K=%lld group=%lld)", fn, (long long)K,
+               (long long)group);
   // Both kernels address A, W, scales and zeros through 32-bit buffer offsets
   // whose out-of-range sentinel is 2^31: every operand must stay below 2 GiB.
   TB_CHECK_ARG(M * K * 2 < (1ll << 31) && K * (N / 2) < (1ll << 31) && (K / group) * N * 2 < (1ll << 31),
-               "tb_w4a16_gemm: A, W and scales must each be smaller than 2 GiB (M=%lld N=%lld K=%lld)",
-               (long long)M, (long long)N, (long long)K);
+               "%s: A, W and scales must each be smaller than 2 GiB (M=%lld N=%lld K=%lld)", fn, (long long)M,
+               (long long)N, (long long)K);
   TB_CHECK_ALIGN(A, 16, "A");
   TB_CHECK_ALIGN(W, 4, "W");
   TB_CHECK_ALIGN(scales, 16, "scales");
   TB_CHECK_ALIGN(zeros, 4, "zeros");
   TB_CHECK_ALIGN(Y, 2, "Y");
   if (M <= 16) {
+    const int64_t slabs = (N + DEC_COLS - 1) / DEC_COLS;
+    const int splits = decode_splits((int)N, (int)K);
+    TB_CHECK_ARG(splits == 1 || (slabs <= DEC_MAX_SLABS && (int64_t)splits * M * N * 4 < (1ll << 31)),
+                 "%s: N=%lld is too wide for the decode kernel", fn, (long long)N);
+  }
+  return TB_OK;
+}
+
+// Launch of the dense W4A16 GEMM after the checks: the split-K decode kernel
+// for M <= 16 (counters at `workspace`, fp32 partials DEC_COUNTER_BYTES past
+// it), the MFMA prefill kernel otherwise.
+static tb_status launch_dense(const char* fn, const uint16_t* A, const uint8_t* W, const uint16_t* scales,
+                              const uint8_t* zeros, uint16_t* Y, int64_t M, int64_t N, int64_t K, int64_t group,
+                              void* workspace, hipStream_t stream) {
+  if (M <= 16) {
+    const int64_t slabs = (N + DEC_COLS - 1) / DEC_COLS;
+    const int splits = decode_splits((int)N, (int)K);
+    int* counters = reinterpret_cast<int*>(workspace);
+    float* partials =
+        splits > 1 ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + DEC_COUNTER_BYTES) : nullptr;
+    if (N % 16 == 0)
+      hipLaunchKernelGGL(w4a16_decode<false>, dim3((unsigned)(slabs * splits)), dim3(DEC_THREADS), 0, stream,
+                         reinterpret_cast<const _Float16*>(A), W, reinterpret_cast<const _Float16*>(scales), zeros,
+                         reinterpret_cast<_Float16*>(Y), partials, counters, (int)M, (int)N, (int)K, (int)group, splits);
+    else
+      hipLaunchKernelGGL(w4a16_decode<true>, dim3((unsigned)(slabs * splits)), dim3(DEC_THREADS), 0, stream,
+                         reinterpret_cast<const _Float16*>(A), W, reinterpret_cast<const _Float16*>(scales), zeros,
+                         reinterpret_cast<_Float16*>(Y), partials, counters, (int)M, (int)N, (int)K, (int)group, splits);
+    return tb::launch_status(fn);
+  }
+  if (tb_status st = tb::reserve_lds(reinterpret_cast<const void*>(&w4a16_prefill), LDS4_BYTES, fn)) return st;
+  const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
+  hipLaunchKernelGGL(w4a16_prefill, dim3(tiles_m * tiles_n), dim3(T4), LDS4_BYTES, stream,
+                     reinterpret_cast<const _Float16*>(A), W, reinterpret_cast<const _Float16*>(scales), zeros,
+                     reinterpret_cast<_Float16*>(Y), (int)M, (int)N, (int)K, (int)group, tiles_m, tiles_n);
+  return tb::launch_status(fn);
+}
+
+// ---------------------------------------------------------------- no-allocation variant
+// The decode's split-K counters and partials live in one file-scope device
+// array per GPU instead of a caller workspace.  Its size is the decode's need
+// at M <= 16 on a 256-CU device: slabs x splits never exceeds the CU count, so
+// the partials hold at most 256 blocks x 16 rows x 256 columns of fp32
+// (4 MiB), behind the 16 KiB of counters.
+constexpr int64_t NOALLOC_SCRATCH_BYTES = DEC_COUNTER_BYTES + 256ll * 16 * DEC_COLS * 4;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+__global__ void __launch_bounds__(256) clear_counters(int* __restrict__ c, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) c[i] = 0;
+}
+
+struct ScratchSlot {
+  void* ptr = nullptr;  // this device's address of `scratch`
+  bool ready = false;
+};
+static std::mutex g_scratch_mu;
+static ScratchSlot g_scratch[64];
+
+// This device's address of `scratch`, looked up once per device (with that
+// device current) by hipGetSymbolAddress: in host code the array's name is
+// only a stand-in, never a device address.  The first call on a device also
+// clears the counters with a kernel on the caller's stream (not hipMemset: the
+// call may be under graph capture); the decode leaves them at zero afterwards.
+static tb_status scratch_of_current_device(const char* fn, hipStream_t stream, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    tb::set_error("%s: no usable current device", fn);
+    return TB_E_HIP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchSlot& slot = g_scratch[dev];
+  if (!slot.ready) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      tb::set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", fn, dev, hipGetErrorString(e));
+      return TB_E_HIP;
+    }
+    const int n = (int)(DEC_COUNTER_BYTES / 4);
+    hipLaunchKernelGGL(clear_counters, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       reinterpret_cast<int*>(p), n);
+    if (tb_status st = tb::launch_status(fn)) return st;
+    slot.ptr = p;
+    slot.ready = true;
+  }
+  *out = slot.ptr;
+  return TB_OK;
+}
+
+}  // namespace w4a16
+}  // namespace tb
+
+extern "C" tb_status tb_w4a16_gemm(const uint16_t* A, const uint8_t* W, const uint16_t* scales, const uint8_t* zeros,
+                                   uint16_t* Y, int64_t M, int64_t N, int64_t K, int64_t group, void* workspace,
+                                   int64_t workspace_bytes, hipStream_t stream) {
+  using namespace tb::w4a16;
+  const char* fn = "tb_w4a16_gemm";
+  if (tb_status st = check_dense_args(fn, A, W, scales, zeros, Y, M, N, K, group)) return st;
+  if (M <= 16) {
     int64_t need = 0;
     tb_w4a16_workspace_size(M, N, K, group, &need);
-    const int splits = decode_splits((int)N, (int)K);
     if (need > 0) {
       TB_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
                    "tb_w4a16_gemm: M=%lld needs a %lld-byte workspace (got %lld)", (long long)M, (long long)need,
@@ -968,28 +1072,28 @@ extern "C" tb_status tb_w4a16_gemm(const uint16_t* A, const uint8_t* W, const ui
         return TB_E_ALIGN;
       }
     }
-    const int64_t slabs = (N + DEC_COLS - 1) / DEC_COLS;
-    TB_CHECK_ARG(splits == 1 || (slabs <= DEC_MAX_SLABS && (int64_t)splits * M * N * 4 < (1ll << 31)),
-                 "tb_w4a16_gemm: N=%lld is too wide for the decode kernel", (long long)N);
-    int* counters = reinterpret_cast<int*>(workspace);
-    float* partials =
-        need > 0 ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + DEC_COUNTER_BYTES) : nullptr;
-    if (N % 16 == 0)
-      hipLaunchKernelGGL(w4a16_decode<false>, dim3((unsigned)(slabs * splits)), dim3(DEC_THREADS), 0, stream,
-                         reinterpret_cast<const _Float16*>(A), W, reinterpret_cast<const _Float16*>(scales), zeros,
-                         reinterpret_cast<_Float16*>(Y), partials, counters, (int)M, (int)N, (int)K, (int)group, splits);
-    else
-      hipLaunchKernelGGL(w4a16_decode<true>, dim3((unsigned)(slabs * splits)), dim3(DEC_THREADS), 0, stream,
-                         reinterpret_cast<const _Float16*>(A), W, reinterpret_cast<const _Float16*>(scales), zeros,
-                         reinterpret_cast<_Float16*>(Y), partials, counters, (int)M, (int)N, (int)K, (int)group, splits);
-    return tb::launch_status("tb_w4a16_gemm(decode)");
   }
-  if (tb_status st = tb::reserve_lds(reinterpret_cast<const void*>(&w4a16_prefill), LDS4_BYTES, "tb_w4a16_gemm")) return st;
-  const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
-  hipLaunchKernelGGL(w4a16_prefill, dim3(tiles_m * tiles_n), dim3(T4), LDS4_BYTES, stream,
-                     reinterpret_cast<const _Float16*>(A), W, reinterpret_cast<const _Float16*>(scales), zeros,
-                     reinterpret_cast<_Float16*>(Y), (int)M, (int)N, (int)K, (int)group, tiles_m, tiles_n);
-  return tb::launch_status("tb_w4a16_gemm");
+  return launch_dense(fn, A, W, scales, zeros, Y, M, N, K, group, workspace, stream);
+}
+
+extern "C" tb_status tb_w4a16_gemm_noalloc(const uint16_t* A, const uint8_t* W, const uint16_t* scales,
+                                           const uint8_t* zeros, uint16_t* Y, int64_t M, int64_t N, int64_t K,
+                                           int64_t group, hipStream_t stream) {
+  using namespace tb::w4a16;
+  const char* fn = "tb_w4a16_gemm_noalloc";
+  if (tb_status st = check_dense_args(fn, A, W, scales, zeros, Y, M, N, K, group)) return st;
+  void* ws = nullptr;
+  if (M <= 16) {
+    int64_t need = 0;
+    tb_w4a16_workspace_size(M, N, K, group, &need);
+    TB_CHECK_ARG(need <= NOALLOC_SCRATCH_BYTES,
+                 "tb_w4a16_gemm_noalloc: M=%lld N=%lld needs %lld bytes of split-K scratch, the static scratch "
+                 "holds %lld (use tb_w4a16_gemm with a workspace)",
+                 (long long)M, (long long)N, (long long)need, (long long)NOALLOC_SCRATCH_BYTES);
+    if (need > 0)
+      if (tb_status st = scratch_of_current_device(fn, stream, &ws)) return st;
+  }
+  return launch_dense(fn, A, W, scales, zeros, Y, M, N, K, group, ws, stream);
 }
 
 extern "C" tb_status tb_moe_w4a16_grouped_gemm(const uint16_t* A, const uint8_t* W, const uint16_t* scales,
