@@ -667,7 +667,9 @@ def main(argv=None) -> int:
             if name == args.op:
                 continue
             r = measure(name, args.steps, args.warmup, with_cpu)
-            suite[name] = {"metric": r["w"]["metric"], "config": r["w"]["config"], "ms": round(r["ms"], 6),
+            suite[name] = {"metric": r["w"]["metric"], "config": {**r["w"]["config"],
+                                                                  "input_sets": r["timing"]["timed_sets"]},
+                           "ms": round(r["ms"], 6), "untimed_replays_before": r["timing"]["untimed_replays_before"],
                            **r["roofline"], "cpu_baseline": r.get("cpu_baseline")}
             print(f"[bench] {name}: {r['ms'] * 1e3:.1f} us/step, {r['roofline']['achieved']} "
                   f"{r['roofline']['unit']}", file=sys.stderr, flush=True)

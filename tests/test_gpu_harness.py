@@ -93,3 +93,11 @@ def test_timer_sample_grouping_matches_launch_count(gpu):
     st = timer.report_benchmark(lambda: x * 2 + 1, (), {}, warmup=1, repeat=3)
     assert st["time_source"] == "kernel timestamps" and st["mode"] == "graph"
     assert st["mean"] <= st["event_mean"]
+
+
+def test_engine_fp8_act_quant_against_the_cpu_reference(gpu):
+    """Bit-exact codes and scales against impl_torch evaluated on the CPU
+    (config verify.reference_device: cpu)."""
+    _say("engine fp8_act_quant config.yaml")
+    rows = engine.run_benchmark_suite("fp8_act_quant", enabled_backends=["hip"])
+    _check_rows(rows)

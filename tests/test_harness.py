@@ -291,3 +291,15 @@ def test_gating_config_carries_the_reference_grid():
     assert len(cases) == 60 and {c["dtype"] for c in cases} == {"fp16", "bf16", "fp32"}
     assert {c["E"] for c in cases} == {128} and {c["k"] for c in cases} == {2}
     assert sorted({c["M"] for c in cases}) == [1024 * i for i in range(1, 21)]
+
+
+def test_reference_device_cpu_runs_the_torch_reference_on_cpu_copies(fake_operator, tmp_path, monkeypatch):
+    cfg = tmp_path / "config.yaml"
+    cfg.write_text("benchmark: {warmup: 1, repeat: 3}\nverify: {atol: 0, rtol: 0, reference_device: cpu}\n"
+                   "case_grid:\n  n: [4]\n  dtype: [fp32]\n")
+    monkeypatch.setattr(engine, "operator_config", lambda op: cfg)
+    ref = sys.modules["tilebench_amd.benchmarks.operators.fakeop.impl_torch"]
+    seen = []
+    monkeypatch.setattr(ref, "run", lambda x, n: seen.append(x.device.type) or x * 2)
+    res = engine.run_benchmark_suite("fakeop", enabled_backends=["hip"], bench_fn=lambda *a, **k: {"mean": 1.0})
+    assert res[0]["hip_ok"] and seen == ["cpu"]

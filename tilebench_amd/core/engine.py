@@ -35,6 +35,22 @@ def _sync():
         torch.cuda.synchronize()
 
 
+def _to_device(x, device):
+    """Tensors of a (nested) tuple moved to `device`; other values as they are."""
+    if isinstance(x, torch.Tensor):
+        return x.to(device)
+    if isinstance(x, (tuple, list)):
+        return type(x)(_to_device(v, device) for v in x)
+    return x
+
+
+def _device_of(inputs):
+    for v in inputs:
+        if isinstance(v, torch.Tensor):
+            return v.device
+    return torch.device("cpu")
+
+
 def _import_impl(operator_name: str, backend: str):
     """The backend's module, or None (with the reason printed) when it cannot load."""
     try:
@@ -96,6 +112,10 @@ def run_benchmark_suite(operator_name, benchmark_overrides=None, enabled_backend
     arch = detect_arch()
     atol, rtol = config_tolerance(verify_cfg, arch)
     per_output = config_per_output(verify_cfg, arch)
+    # verify.reference_device: cpu runs the torch reference on CPU copies of the
+    # inputs (its IEEE arithmetic) for the correctness check; torch_ms still
+    # times it on the GPU inputs
+    ref_on_cpu = str(verify_cfg.get("reference_device", "")).lower() == "cpu"
     timing = timing_mode(use_graph) if HAS_CUDA else None
 
     cases = expand_cases(operator_name, config)
@@ -133,7 +153,10 @@ def run_benchmark_suite(operator_name, benchmark_overrides=None, enabled_backend
             print(f"  Skipped: input generation failed ({type(e).__name__}: {e})")
             continue
         try:
-            ref_output = impl_torch.run(*inputs)
+            if ref_on_cpu:
+                ref_output = _to_device(impl_torch.run(*_to_device(inputs, "cpu")), _device_of(inputs))
+            else:
+                ref_output = impl_torch.run(*inputs)
             _sync()
         except (RuntimeError, TypeError, ValueError) as e:
             print(f"  Skipped: reference failed ({type(e).__name__}: {e})")

@@ -62,7 +62,9 @@ def compute_derived(result: dict, metrics_cfg: dict, peak_cfg: dict | None = Non
     peak_bw = peak.get("peak_bw_GBs") or metrics_cfg.get("peak_bw_GBs")
     peak_bw = float(peak_bw) if peak_bw is not None else None
     peak_mode = metrics_cfg.get("peak_tflops_key") or result.get("dtype")
-    raw = {**(peak.get("peak_tops") or {}), **(peak.get("peak_tflops") or {})}.get(peak_mode)
+    table = {**(peak.get("peak_tops") or {}), **(peak.get("peak_tflops") or {})}
+    # a case dtype names its matrix peak with the calibration's "_mma" suffix
+    raw = table.get(peak_mode, table.get(f"{peak_mode}_mma"))
     peak_tf = float(raw) if raw is not None else None
     torch_ms = result.get("torch_ms")
     torch_ms = float(torch_ms) if torch_ms is not None and torch_ms > 0 and not math.isnan(torch_ms) else None
