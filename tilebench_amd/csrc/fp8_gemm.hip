@@ -6,18 +6,31 @@
 // CDNA4 fp8 matrix cores (v_mfma_f32_32x32x64_f8f6f4, e4m3 x e4m3), one
 // rounding to bf16 (RNE) after both scales.
 //
-// One 256 x 256 output tile per 512-thread block, eight wavefronts (two per
-// SIMD) each owning a 128 x 64 sub-tile (8 fp32 32x32 accumulators), K advanced
-// 128 bytes at a time.  Both operands stream HBM -> LDS through the buffer
-// unit (buffer_load ... lds, no registers) one step ahead, two LDS stages of
-// [256][128 B] per operand.  Rows are split in 16-byte chunks, chunk c of row r
-// at slot c ^ ((r ^ (r >> 3)) & 7), so the DMA writes (contiguous) and the
-// fragment reads (eight consecutive rows at one chunk) are conflict-free.  A
-// fragment of the 32x32x64 MFMA is 32 consecutive bytes of one row (two
-// ds_read_b128); A and B use the same k order, which is all a dot product needs.
-// The epilogue scales, rounds to bf16, stages the tile in LDS and writes
-// 16-byte row chunks.  Tiles are numbered XCD-aware as in the W4A16 kernel.
+// One 256 x 256 output tile per 256-thread block: four wavefronts, one per
+// SIMD, each owning a 128 x 128 sub-tile (16 fp32 32x32 accumulators, 256
+// accumulator registers).  K advances 128 bytes per step, in two 64-byte
+// substeps.  Both operands stream HBM -> LDS through the buffer unit
+// (buffer_load ... lds, no registers), two LDS stages of [256][128 B] per
+// operand; rows are 16-byte chunks, chunk c of row r at slot
+// c ^ ((r ^ (r >> 3)) & 7), so the DMA writes and the fragment reads are
+// conflict-free.
+//
+// The matrix pipe never waits on LDS: while the 16 MFMAs of one substep run,
+// the wavefront reads the fragments of the next substep (one ds_read_b128 per
+// MFMA).  One barrier per step sits between the two substeps: before it every
+// wavefront has finished reading the current stage and has waited for its
+// share of the next stage's DMA, so after it the current stage's buffer takes
+// the DMA of step k + 2 (issued between the second substep's MFMAs) and the
+// next stage's first fragments can be read while the second substep runs.
+//
+// The MFMA computes the transposed product (W^T fragment first), so a lane
+// holds four consecutive output columns of one row per group of four
+// accumulator elements; the epilogue scales, rounds to bf16, stages the tile
+// in LDS with 8-byte writes and stores 16-byte row chunks.  Tiles are numbered
+// XCD-aware as in the W4A16 kernel.
 #include "tb_common.h"
+
+#include <type_traits>
 
 namespace tb {
 namespace fp8gemm {
@@ -25,8 +38,9 @@ namespace fp8gemm {
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 
-constexpr int BM = 256, BN = 256, BK = 128, THREADS = 512, GROUP_M = 8;
+constexpr int BM = 256, BN = 256, BK = 128, THREADS = 256, GROUP_M = 8;
 constexpr int STAGE = BM * BK;  // bytes per operand stage
 constexpr int C_STRIDE = BN + 8;  // bf16 elements per staged output row (16-byte pad)
 // A and B, two stages each (128 KiB), reused for the staged bf16 output tile.
@@ -37,10 +51,12 @@ constexpr uint32_t OOB = 0x80000000u;
 
 __device__ __forceinline__ int slot(int row, int chunk) { return row * BK + ((chunk ^ ((row ^ (row >> 3)) & 7)) << 4); }
 
-__device__ __forceinline__ uint16_t bf16_rne(float f) {
+// fp32 -> bf16 bits, round to nearest even, NaN kept quiet; a select, not a
+// branch, so the epilogue's 256 conversions per lane stay straight-line code.
+__device__ __forceinline__ uint32_t bf16_rne_sel(float f) {
   const uint32_t b = __builtin_bit_cast(uint32_t, f);
-  if ((b & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((b >> 16) | 0x40u);
-  return (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+  const uint32_t r = (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+  return (b & 0x7FFFFFFFu) > 0x7F800000u ? ((b >> 16) | 0x40u) : r;
 }
 
 struct Tile {
@@ -91,17 +107,17 @@ __global__ void __launch_bounds__(THREADS, 1)
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const Tile tile = tile_of_block(tiles_m, tiles_n);
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = wave >> 1, wn = wave & 1;
 
   const i32x4 ra = make_rsrc4(Aq, (uint32_t)M * (uint32_t)K);
   const i32x4 rb = make_rsrc4(WqT, (uint32_t)N * (uint32_t)K);
-  // DMA: per operand and step, 32 instructions of 1 KiB (8 rows); wave w issues 4.
-  uint32_t a_off[4], b_off[4];
+  // DMA: per operand and stage, 32 instructions of 1 KiB (8 rows); wave w issues 8 of each.
+  uint32_t a_off[8], b_off[8];
   {
     const int lr = lane >> 3;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = (wave * 4 + i) * 8 + lr;
+    for (int i = 0; i < 8; ++i) {
+      const int row = (wave * 8 + i) * 8 + lr;
       const int lc = (lane & 7) ^ ((row ^ (row >> 3)) & 7);
       const int m = tile.m0 + row, n = tile.n0 + row;
       a_off[i] = m < M ? (uint32_t)m * (uint32_t)K + (uint32_t)lc * 16u : OOB;
@@ -110,114 +126,156 @@ __global__ void __launch_bounds__(THREADS, 1)
   }
   const uint32_t lds0 = (uint32_t)__builtin_amdgcn_readfirstlane(
       (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
-  auto issue = [&](int kt) {
-    const uint32_t st = lds0 + (uint32_t)((kt & 1) * 2 * STAGE) + (uint32_t)(wave * 4 * 1024);
+  // LDS layout [A stage 0 | A stage 1 | B stage 0 | B stage 1], 32 KiB each.
+  // DMA instruction q (0..15) of step kt: A rows for q < 8, B rows for q >= 8.
+  auto dma = [&](int kt, int q) {
+    const uint32_t st = lds0 + (uint32_t)((kt & 1) * STAGE) + (uint32_t)(wave * 8 * 1024);
     const uint32_t soff = (uint32_t)(kt * BK);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(st + i * 1024, a_off[i], ra, soff);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(st + STAGE + i * 1024, b_off[i], rb, soff);
+    if (q < 8)
+      dma16(st + q * 1024, a_off[q], ra, soff);
+    else
+      dma16(st + 2 * STAGE + (q - 8) * 1024, b_off[q - 8], rb, soff);
   };
 
-  // Fragment reads: row base + i*32 + (lane & 31); k substep s covers chunks
-  // 4s + 2h, 4s + 2h + 1 with h = lane / 32.
+  // Fragment f (0..3 A rows, 4..7 B rows) of substep s: row base + (f & 3) * 32
+  // + lane % 32, chunks 4s + 2h and 4s + 2h + 1 with h = lane / 32 (32 bytes).
+  // Rows 32 apart differ in bit 2 of (row >> 3) only, so the swizzle depends on
+  // f & 1: per operand, substep and half, two base addresses (f even / odd)
+  // cover all four fragments with immediate offsets (8 KiB apart), and the
+  // stage (32 KiB) is an immediate too.
   const int a_row = wm * 128 + (lane & 31);
-  const int b_row = wn * 64 + (lane & 31);
+  const int b_row = wn * 128 + (lane & 31);
+  uint32_t abase[2][2][2], bbase[2][2][2];  // [s][half][f & 1]
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int par = 0; par < 2; ++par) {
+        const int c = 4 * s2 + 2 * (lane >> 5) + hf;
+        abase[s2][hf][par] = (uint32_t)slot(a_row + par * 32, c);
+        bbase[s2][hf][par] = (uint32_t)(2 * STAGE + slot(b_row + par * 32, c));
+      }
+  auto frag = [&](auto stage, int f, int s2) -> i32x8 {
+    constexpr int ST = decltype(stage)::value * STAGE;
+    const uint32_t* bs = f < 4 ? &abase[s2][0][0] : &bbase[s2][0][0];
+    const int par = f & 1, off = ST + ((f & 3) >> 1) * 8192;
+    const i32x4 lo = *reinterpret_cast<const i32x4*>(lds + bs[0 * 2 + par] + off);
+    const i32x4 hi = *reinterpret_cast<const i32x4*>(lds + bs[1 * 2 + par] + off);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
 
-  f32x16 acc[4][2];
+  f32x16 acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
-  auto frag = [&](const uint8_t* base, int row, int s) -> i32x8 {
-    const int c0 = 4 * s + 2 * (lane >> 5);
-    const i32x4 lo = *reinterpret_cast<const i32x4*>(base + slot(row, c0));
-    const i32x4 hi = *reinterpret_cast<const i32x4*>(base + slot(row, c0 + 1));
-    i32x8 r;
-    r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
-    r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
-    return r;
+  // Fragment registers of one substep: 4 A and 4 B fragments of 8 dwords.
+  i32x8 cur[8], nxt[8];
+  // 16 MFMAs (4 A x 4 B fragments); after MFMA q, body(q) issues interleaved work.
+  auto mfma_all = [&](i32x8 (&fr)[8], auto body) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // transposed product: W^T fragment first, so a lane holds 4 consecutive columns
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fr[4 + j], fr[i], acc[i][j], 0, 0, 0, 0, 0, 0);
+        body(i * 4 + j);
+      }
   };
 
   constexpr int WAIT_VM0 = 0 | (7 << 4) | (15 << 8);
+  constexpr int WAIT_VM16_LGKM0 = 0 | (7 << 4) | (0 << 8) | (1 << 14);  // vmcnt(16), lgkmcnt(0)
   const int nk = K / BK;
-  issue(0);
-  __builtin_amdgcn_s_waitcnt(WAIT_VM0);
+  // Prologue: stages 0 and 1 in flight, wait for stage 0, read its substep-0 fragments.
+#pragma unroll
+  for (int q = 0; q < 16; ++q) dma(0, q);
+  if (nk > 1) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) dma(1, q);
+    __builtin_amdgcn_s_waitcnt(WAIT_VM16_LGKM0);
+  } else {
+    __builtin_amdgcn_s_waitcnt(WAIT_VM0);
+  }
   __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const bool more = kt + 1 < nk;
-    if (more) issue(kt + 1);
-    const uint8_t* sa_ = lds + (kt & 1) * 2 * STAGE;
-    const uint8_t* sb_ = sa_ + STAGE;
-    {
-      // Both k64 substeps' fragments are read up front; the scheduling hints
-      // then interleave the second substep's 12 LDS reads with the first
-      // substep's MFMAs, so the matrix pipe does not wait on LDS latency.
-      i32x8 fa0[4], fb0[2], fa1[4], fb1[2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) fa0[i] = frag(sa_, a_row + i * 32, 0);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) fb0[j] = frag(sb_, b_row + j * 32, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) fa1[i] = frag(sa_, a_row + i * 32, 1);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) fb1[j] = frag(sb_, b_row + j * 32, 1);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa0[i], fb0[j], acc[i][j], 0, 0, 0, 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa1[i], fb1[j], acc[i][j], 0, 0, 0, 0, 0, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);  // substep-0 fragment reads
-#pragma unroll
-      for (int q = 0; q < 6; ++q) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two substep-1 reads
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 10, 0);
-    }
-    // Stage kt+1 (issued above, 8 DMA per lane) must land before the barrier
-    // that hands it to the next step.
-    if (more) __builtin_amdgcn_s_waitcnt(WAIT_VM0);
-    __syncthreads();
-  }
+  for (int f = 0; f < 8; ++f) cur[f] = frag(std::integral_constant<int, 0>{}, f, 0);
 
-  // Epilogue: element e of fragment (i, j) is row i*32 + (e/4)*8 + (lane/32)*4 + e%4,
-  // column j*32 + lane%32 of the wave tile.
-  uint16_t* ct = reinterpret_cast<uint16_t*>(lds);
-  const int rbase = wm * 128 + (lane >> 5) * 4;
-  const int cbase = wn * 64 + (lane & 31);
-  // Scales by buffer loads with out-of-range offsets past M or N (zeros): no
-  // branch around a load, so the 66 loads of a lane are in flight together
-  // instead of one round trip each.
-  const buf_rsrc_t rsa = buf_rsrc(sa, (uint32_t)M * 4u), rsw = buf_rsrc(sw, (uint32_t)N * 4u);
-  float swv[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = tile.n0 + cbase + j * 32;
-    swv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsw, n < N ? (uint32_t)n * 4u : OOB, 0, 0));
+  // Step kt on stage SB = kt & 1 (a compile-time constant: the loop runs two
+  // steps per iteration).
+  auto step = [&](int kt, auto sbc) {
+    constexpr int SB = decltype(sbc)::value;
+    const std::integral_constant<int, SB> cur_st{};
+    const std::integral_constant<int, SB ^ 1> nxt_st{};
+    // substep 0: MFMAs on `cur`; one fragment of substep 1 of this stage read
+    // into `nxt` after every second MFMA.  The scheduling barriers keep this
+    // order: MFMAs are asynchronous, so the reads go out while they run.
+    mfma_all(cur, [&](int q) {
+      if ((q & 1) == 0) nxt[q >> 1] = frag(cur_st, q >> 1, 1);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    // this stage is fully read; the next one must have landed (each wave waits
+    // for its own DMA, the barrier publishes all of them)
+    __builtin_amdgcn_s_waitcnt(WAIT_VM0);
+    __syncthreads();
+    // substep 1: MFMAs on `nxt`; the next stage's substep-0 fragments read into
+    // `cur`; the DMA of step kt + 2 refills this stage's buffer.  Past the last
+    // steps both still go out: a stale stage is read into registers nobody
+    // uses, and the DMA past K fetches in-bounds bytes (or zeros past the
+    // buffer) into a stage nobody reads.
+    mfma_all(nxt, [&](int q) {
+      if ((q & 1) == 0) cur[q >> 1] = frag(nxt_st, q >> 1, 0);
+      dma(kt + 2, q);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+  int kt = 0;
+  for (; kt + 1 < nk; kt += 2) {
+    step(kt, std::integral_constant<int, 0>{});
+    step(kt + 1, std::integral_constant<int, 1>{});
   }
-  float sav[4][16];
+  if (kt < nk) step(kt, std::integral_constant<int, 0>{});
+  __builtin_amdgcn_s_waitcnt(WAIT_VM0);  // the DMAs issued past the end, before LDS is reused
+
+  // Epilogue: with the transposed product, element e of fragment (i, j) is
+  // row i*32 + lane%32, column j*32 + (e/4)*8 + (lane/32)*4 + e%4 of the wave tile.
+  __syncthreads();  // every wave is done with the stages before they hold the output tile
+  uint16_t* ct = reinterpret_cast<uint16_t*>(lds);
+  const buf_rsrc_t rsa = buf_rsrc(sa, (uint32_t)M * 4u), rsw = buf_rsrc(sw, (uint32_t)N * 4u);
+  float sav[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = tile.m0 + wm * 128 + i * 32 + (lane & 31);
+    sav[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsa, m < M ? (uint32_t)m * 4u : OOB, 0, 0));
+  }
+  float swv[4][4][4];  // [j][g][e]: column j*32 + g*8 + (lane/32)*4 + e
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int n = tile.n0 + wn * 128 + j * 32 + g * 8 + (lane >> 5) * 4 + e;
+        swv[j][g][e] =
+            __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsw, n < N ? (uint32_t)n * 4u : OOB, 0, 0));
+      }
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int m = tile.m0 + rbase + i * 32 + (e >> 2) * 8 + (e & 3);
-      sav[i][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsa, m < M ? (uint32_t)m * 4u : OOB, 0, 0));
-    }
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+      for (int g = 0; g < 4; ++g) {
+        const int row = wm * 128 + i * 32 + (lane & 31);
+        const int col = wn * 128 + j * 32 + g * 8 + (lane >> 5) * 4;
+        uint32_t h[4];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int row = rbase + i * 32 + (e >> 2) * 8 + (e & 3);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) ct[row * C_STRIDE + cbase + j * 32] = bf16_rne(acc[i][j][e] * sav[i][e] * swv[j]);
-    }
+        for (int e = 0; e < 4; ++e) h[e] = bf16_rne_sel(acc[i][j][4 * g + e] * sav[i] * swv[j][g][e]);
+        u32x2v v;
+        v[0] = h[0] | (h[1] << 16);
+        v[1] = h[2] | (h[3] << 16);
+        *reinterpret_cast<u32x2v*>(ct + row * C_STRIDE + col) = v;
+      }
   __syncthreads();
   const int rows = min(BM, M - tile.m0);
   const int cols = min(BN, N - tile.n0);
