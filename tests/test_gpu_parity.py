@@ -287,6 +287,24 @@ def test_w4a16_gemm_full_prefill(gpu):
     np.testing.assert_allclose(Yc[rows].astype(np.float32), ref.astype(np.float32), atol=1e-2, rtol=1e-2)
 
 
+def test_w4a16_prefill_192_row_tail(gpu):
+    """M = 3000, N = 11008: 12 x 43 = 516 tiles of 256 x 256 would leave a third
+    round of 4 tiles on 256 CUs, so the launch covers the last tile column with
+    16 tiles of 192 rows instead (the last one ragged: rows 2880 .. 2999).
+    Rows from every part, the ragged rows included, against the oracle."""
+    from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip
+
+    M, K, N, G = 3000, 512, 11008, 128
+    _say("w4a16_gemm prefill with 192-row tail tiles", M, K, N, G)
+    A, p, s, z, G = T.generate_w4a16_gemm_inputs(M, K, N, G, seed=5, device="cpu")
+    Y = impl_hip.run(A.to(gpu), p.to(gpu), s.to(gpu), z.to(gpu), G)
+    torch.cuda.synchronize()
+    Yc = Y.cpu().numpy()
+    rows = np.concatenate([np.random.default_rng(1).choice(2880, 64, replace=False), np.arange(2880, 3000)])
+    ref = oracle.w4a16_gemm(A.numpy()[rows], p.numpy(), s.numpy(), z.numpy(), G)
+    np.testing.assert_allclose(Yc[rows].astype(np.float32), ref.astype(np.float32), atol=1e-2, rtol=1e-2)
+
+
 def test_w4a16_decode_repeat_calls_reuse_workspace(gpu):
     """The split-K counters must be back at zero after each call: three calls in a row agree."""
     from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip

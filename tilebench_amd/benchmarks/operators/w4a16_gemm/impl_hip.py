@@ -34,7 +34,7 @@ def run(A: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, zeros: torc
     rt.call("tb_w4a16_gemm", A.data_ptr(), packed.data_ptr(), scales.data_ptr(), zeros.data_ptr(), Y.data_ptr(),
             M, N, K, group, rt.ptr(ws), need.value, stream)
     _last_config = ({"kernel": "w4a16_decode", "cols_per_block": 256, "workspace_bytes": need.value}
-                    if M <= 16 else {"kernel": "w4a16_prefill", "BM": 256, "BN": 256, "BK": 64, "waves": 4})
+                    if M <= 16 else {"kernel": "w4a16_prefill", "BM": 256, "BN": 256, "BK": 64, "waves": 8})
     return Y
 
 

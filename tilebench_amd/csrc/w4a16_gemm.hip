@@ -3,7 +3,38 @@
 // A is fp16 row-major; W is int4 in the N-packed, low-nibble-first layout with
 // group-wise fp16 scales and int4 zero-points along K (see include/tbhip.h).
 //
-// Prefill kernel (MFMA-bound for large M): one 256 x 256 output tile per
+// Dense prefill (w4a16_prefill, MFMA-bound for large M): one 256 x 256 output
+// tile per 512-thread block, eight wavefronts (two per SIMD); wavefront
+// (wm, wn) owns rows 128 wm .. +127 and columns 64 wn .. +63 as 4 x 2
+// v_mfma_f32_32x32x16_f16 accumulators.  Its two 32-column fragments are the
+// even and the odd columns of its range: lane l owns packed byte l % 32 of
+// the range, so one byte per K row carries both of its columns.
+//
+//   A, W  : the A tile ([256][64 halfs]), the packed W tile ([64][128 B]) and
+//           the step's group of scales and zero-points stream HBM -> LDS by
+//           the buffer unit (buffer_load ... lds), three stages, issued two
+//           steps ahead; a wavefront waits only for its own share of the next
+//           stage, and one barrier per step publishes it;
+//   W     : never stored in fp16: per k16 slice one ds_read_b64_tr_b8 (the
+//           gfx950 transposing LDS read) hands each lane its byte column for 8
+//           consecutive k rows, and the lane dequantises in registers with the
+//           standalone dequantiser's exact arithmetic ((1024 + q) and (64 + q)
+//           half2 from the 0x64 / 0x54 magic numbers, exact zero-point
+//           subtraction, one RNE multiply by the scale);
+//   MFMA  : while the 8 MFMAs of one slice run, the wavefront reads and
+//           dequantises the next slice; the DMA of step k + 3 is issued
+//           between the MFMAs that follow the step's barrier;
+//   output: each lane holds 8 consecutive columns of one row per accumulator
+//           group (even and odd accumulators interleaved): 16-byte stores
+//           straight from the accumulators.
+//   rounds: a launch of T tiles on C CUs runs ceil(T / C) rounds; when the
+//           last round would be part-empty, the host may cover the last tile
+//           columns with 192-row tiles instead, so that the work splits into
+//           whole rounds more evenly.
+// Every output element sees the same MFMA operands, in the same K order, as
+// in prefill_tile below, so the two kernels give bit-identical results.
+//
+// Grouped and MoE kernels (prefill_tile): one 256 x 256 output tile per
 // 512-thread block, eight wavefronts (two per SIMD) each owning a 128 x 64
 // sub-tile (8 v_mfma_f32_32x32x16_f16 accumulators = 128 fp32 per lane), K
 // advanced 64 at a time:
@@ -42,6 +73,8 @@
 #include "tb_common.h"
 
 #include <algorithm>
+#include <functional>
+#include <vector>
 #include <mutex>
 #include <type_traits>
 
@@ -489,15 +522,6 @@ __device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _
   }
 }
 
-__global__ void __launch_bounds__(T4, 1)
-    w4a16_prefill(const _Float16* __restrict__ A, const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
-                  const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int M, int N, int K, int group,
-                  int tiles_m, int tiles_n) {
-  extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
-  const Tile tile = tile_of_block(tiles_m, tiles_n);
-  prefill_tile<A_DIRECT, EPI_PLAIN>(lds, A, W, S, Z, Y, M, tile.m0, M, tile.n0, N, K, group);
-}
-
 // Expert and row range of grouped tile row mt: rows offsets[e] .. offsets[e+1]
 // of the row space (R rows) use expert e, cut into 256-row tiles.  Offsets are
 // clamped to [0, R] so that malformed ones never address rows outside A / Y.
@@ -919,6 +943,348 @@ inline int decode_splits(int N, int K) {
   return std::max(s, 1);
 }
 
+// ---------------------------------------------------------------- dense prefill
+namespace p8 {
+constexpr int THREADS = 512, STAGES = 3;
+constexpr int A_ST = BM * BK * 2;         // 32 KiB: [256 rows][128 B]
+constexpr int W_ROWS = BK * BN / 2;       // 8 KiB:  [64 rows][128 B] packed int4
+constexpr int S_OFF = W_ROWS;             // 512 B: the step's group scales, 256 fp16
+constexpr int Z_OFF = S_OFF + BN * 2;     // 256 B: its zero-points (128 B) + 128 B landing pad
+constexpr int PAD_OFF = Z_OFF + 256;      // 256 B: landing pad of the idle wavefronts' DMA
+constexpr int W_ST = PAD_OFF + 256;       // 9 KiB per W stage
+constexpr int STAGE = A_ST + W_ST;
+constexpr size_t LDS_BYTES = (size_t)STAGES * STAGE;  // 123 KiB
+static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+
+typedef int v2i __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void dma16(uint32_t lds_addr, uint32_t voff, const i32x4& rsrc, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane((int)lds_addr)), "v"(voff), "s"(rsrc),
+                 "s"(__builtin_amdgcn_readfirstlane((int)soff))
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(uint32_t lds_addr, uint32_t voff, const i32x4& rsrc, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane((int)lds_addr)), "v"(voff), "s"(rsrc),
+                 "s"(__builtin_amdgcn_readfirstlane((int)soff))
+               : "memory", "m0");
+}
+// Block ids go round-robin to the 8 XCDs: regroup ids so that each XCD owns
+// a contiguous run of tiles (when the count is a multiple of 8).
+__device__ __forceinline__ int remap_xcd(int bid, int nb) {
+  return (nb & 7) == 0 ? (bid & 7) * (nb >> 3) + (bid >> 3) : bid;
+}
+// Tile idx of a tiles_m x tiles_n grid of (rows x 256) tiles, in groups of
+// GROUP_M tile rows (L2 reuse), columns offset by n_base.
+__device__ __forceinline__ Tile tile_in_grid(int idx, int tiles_m, int tiles_n, int rows, int n_base) {
+  const int per_group = GROUP_M * tiles_n;
+  const int group = idx / per_group;
+  const int first_m = group * GROUP_M;
+  const int in_rows = min(tiles_m - first_m, GROUP_M);
+  const int in_group = idx - group * per_group;
+  Tile t;
+  t.m0 = (first_m + in_group % in_rows) * rows;
+  t.n0 = n_base + (in_group / in_rows) * BN;
+  return t;
+}
+__device__ __forceinline__ Tile tile_of(int bid, int nb, int tiles_m, int tiles_n, int rows, int n_base) {
+  return tile_in_grid(remap_xcd(bid, nb), tiles_m, tiles_n, rows, n_base);
+}
+__device__ __forceinline__ i32x4 rsrc4(const void* p, uint32_t bytes) {
+  const uint64_t base = (uint64_t)(uintptr_t)p;
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)base);
+  r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(base >> 32) & 0xFFFF);
+  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  r[3] = (int)RSRC_DW3;
+  return r;
+}
+// (x & mask) | c in one instruction: mask from a scalar register, c from a vector one
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(c));
+  return r;
+}
+
+// One tile of 64 MB rows (MB = 4: 256, MB = 3: 192) x 256 columns at (m0, n0).
+template <int MB>
+__device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16* __restrict__ A,
+                                      const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
+                                      const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int M, int N, int K,
+                                      int group, const Tile tile) {
+  constexpr int TM = 64 * MB;       // tile rows
+  constexpr int AI = MB;            // A DMA instructions per wavefront and step (8 rows each)
+  constexpr int DMA_PER_STEP = AI + 5;
+  const int t = threadIdx.x, lane = t & 63, h = lane >> 5, j = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = w >> 2, wn = w & 3;
+  const int nk = K / BK;
+  const uint32_t half_n = (uint32_t)(N / 2);
+
+  const i32x4 ra = rsrc4(A, (uint32_t)M * (uint32_t)K * 2u);
+  const i32x4 rw = rsrc4(W, (uint32_t)K * half_n);
+  const i32x4 rs = rsrc4(S, (uint32_t)(K / group) * (uint32_t)N * 2u);
+  const i32x4 rz = rsrc4(Z, (uint32_t)(K / group) * half_n);
+
+  // A DMA: instruction i of wavefront w fills rows 8 (AI w + i) .. +7 (lane
+  // L: row + L / 8, 16-byte slot L % 8, which holds chunk slot ^ swizzle).
+  uint32_t a_off[AI];
+#pragma unroll
+  for (int i = 0; i < AI; ++i) {
+    const int row = 8 * (AI * w + i) + (lane >> 3);
+    const int c = (lane & 7) ^ ((row ^ (row >> 3)) & 7);
+    const int m = tile.m0 + row;
+    a_off[i] = m < M ? ((uint32_t)m * (uint32_t)K + (uint32_t)c * 8u) * 2u : OOB;
+  }
+  // W DMA: instruction i of wavefront w fills rows 8w + 2i, +1 (lane L: row +
+  // L / 32, dword L % 32 of the row, i.e. 16-byte slot (L % 32) / 4, which
+  // holds chunk slot ^ (row & 7)).
+  uint32_t w_off[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 8 * w + 2 * i + (lane >> 5);
+    const int c = ((lane & 31) >> 2) ^ (r & 7);
+    const uint32_t col = (uint32_t)(tile.n0 / 2 + c * 16 + (lane & 3) * 4);
+    w_off[i] = col < half_n ? (uint32_t)r * half_n + col : OOB;
+  }
+  // Scales and zero-points of a step's group: wavefronts 0 and 1 fetch the
+  // 512 scale bytes, wavefront 2 the 128 zero-point bytes (lanes 32..63 land
+  // in the pad), the others nothing (their lanes land in the pad).
+  uint32_t sz_off = OOB, sz_lds = PAD_OFF;
+  const i32x4& rsz = w == 2 ? rz : rs;
+  if (w < 2) {
+    const uint32_t col = (uint32_t)tile.n0 + (uint32_t)(w * 128 + lane * 2);
+    sz_off = col < (uint32_t)N ? col * 2u : OOB;
+    sz_lds = S_OFF + w * 256;
+  } else if (w == 2) {
+    const uint32_t col = (uint32_t)(tile.n0 / 2 + lane * 4);
+    sz_off = lane < 32 && col < half_n ? col : OOB;
+    sz_lds = Z_OFF;
+  }
+  const uint32_t lds0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)(
+      __attribute__((address_space(3))) void*)lds);
+
+  // DMA of step ks into stage st (out-of-range offsets past the last step:
+  // nothing is read, the stage is not used again).
+  // DMA instruction d (0 .. 8) of step ks into stage st
+  auto issue_one = [&](int ks, int st, int d) __attribute__((always_inline)) {
+    const bool live = ks < nk;
+    const uint32_t sb = lds0 + (uint32_t)(st * STAGE);
+    if (d < AI) {
+      dma16(sb + (uint32_t)(8 * (AI * w + d) * 128), live ? a_off[d] : OOB, ra, (uint32_t)(ks * BK) * 2u);
+    } else if (d < AI + 4) {
+      dma4(sb + (uint32_t)(A_ST + (8 * w + 2 * (d - AI)) * 128), live ? w_off[d - AI] : OOB, rw,
+           (uint32_t)(ks * BK) * half_n);
+    } else {
+      const uint32_t g = (uint32_t)(ks * BK) / (uint32_t)group;
+      const uint32_t ss = w == 2 ? g * half_n : g * (uint32_t)N * 2u;
+      dma4(sb + (uint32_t)A_ST + sz_lds, live ? sz_off : OOB, rsz, ss);
+    }
+  };
+  auto issue = [&](int ks, int st) __attribute__((always_inline)) {
+    const bool live = ks < nk;
+    const uint32_t sb = lds0 + (uint32_t)(st * STAGE);
+    const uint32_t sa = (uint32_t)(ks * BK) * 2u;
+#pragma unroll
+    for (int i = 0; i < AI; ++i) dma16(sb + (uint32_t)(8 * (AI * w + i) * 128), live ? a_off[i] : OOB, ra, sa);
+    const uint32_t sw = (uint32_t)(ks * BK) * half_n;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma4(sb + (uint32_t)(A_ST + (8 * w + 2 * i) * 128), live ? w_off[i] : OOB, rw, sw);
+    const uint32_t g = (uint32_t)(ks * BK) / (uint32_t)group;
+    const uint32_t ss = w == 2 ? g * half_n : g * (uint32_t)N * 2u;
+    dma4(sb + (uint32_t)A_ST + sz_lds, live ? sz_off : OOB, rsz, ss);
+  };
+
+  // A fragment mb of slice c: row 32 (MB wm + mb) + j, chunk 2c + h; its
+  // swizzle depends on the row's 32-row block through bit 2 only (parity
+  // of MB wm + mb).
+  uint32_t fa_off[4][2];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+      const int sw = (j ^ (4 * par + (j >> 3))) & 7;
+      fa_off[c][par] = (uint32_t)(wm * MB * 4096 + j * 128 + (((2 * c + h) ^ sw) << 4));
+    }
+  // Transposing byte read of slice c: lane p = 2r + b of its group of 16
+  // (group G = lane / 16: columns 16 (G & 1) .., rows 8 (G >> 1) ..) points at
+  // row 16c + 8 (G >> 1) + r, bytes 32 wn + 16 (G & 1) + 8b .. +7.
+  uint32_t wt_off;
+  {
+    const int p = lane & 15, r = p >> 1, b = p & 1, G = lane >> 4;
+    const int cb = 2 * wn + (G & 1);
+    wt_off = (uint32_t)(A_ST + (8 * (G >> 1) + r) * 128 + ((cb ^ r) << 4) + 8 * b);
+  }
+
+  f32x16 acc[MB][2];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) acc[i][0] = acc[i][1] = f32x16{};
+
+  // magic-number words in registers (a VOP3 instruction takes one scalar operand)
+  const uint32_t c64 = __builtin_amdgcn_readfirstlane(0x64006400u) + (uint32_t)(lane >> 6);
+  const uint32_t c54 = __builtin_amdgcn_readfirstlane(0x54005400u) + (uint32_t)(lane >> 6);
+  h8 fa[2][MB];
+  h8 wf[2][2];
+  uint32_t sE = 0, sO = 0, zE = 0, zO = 0;  // half2 {s, s} / {1024 + z, 1024 + z} / {64 + z, 64 + z}
+
+  auto load_scales = [&](int st) __attribute__((always_inline)) {
+    const uint8_t* sb = lds + st * STAGE + A_ST;
+    const uint32_t s2 = *reinterpret_cast<const uint32_t*>(sb + S_OFF + (wn * 64 + 2 * j) * 2);
+    const uint32_t zb = sb[Z_OFF + wn * 32 + j];
+    sE = perm(s2, s2, 0x01000100u);
+    sO = perm(s2, s2, 0x03020302u);
+    const uint32_t zz = zb | (zb << 16);
+    zE = (zz & 0x000F000Fu) | 0x64006400u;
+    zO = (zz & 0x00F000F0u) | 0x54005400u;
+  };
+  auto read_a = [&](int st, int c, int buf, int mb) __attribute__((always_inline)) {
+    typedef __attribute__((address_space(3))) uint8_t lds_u8;
+    lds_u8* const base = (lds_u8*)(__attribute__((address_space(3))) void*)lds;
+    fa[buf][mb] = *(__attribute__((address_space(3))) const h8*)(base + fa_off[c][(MB * wm + mb) & 1] +
+                                                                   (st * STAGE + mb * 4096));
+  };
+  auto read_w = [&](int st, int c) __attribute__((always_inline)) -> v2i {
+    typedef __attribute__((address_space(3))) uint8_t lds_u8;
+    lds_u8* const base = (lds_u8*)(__attribute__((address_space(3))) void*)lds;
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+        (__attribute__((address_space(3))) v2i*)(base + st * STAGE + c * 2048 + wt_off));
+  };
+  // k-row pairs (2q, 2q + 1) as {byte 2q, 0, byte 2q + 1, 0}; the even
+  // column's nibbles under 0x64 read 1024 + q, the odd column's (bits 7:4)
+  // under 0x54 read 64 + q.
+  auto dequant_pair = [&](const v2i x, int buf, int q, u32x4& e, u32x4& o) __attribute__((always_inline)) {
+    const uint32_t src = (uint32_t)x[q >> 1];
+    const uint32_t d = perm(src, src, (q & 1) ? 0x0C030C02u : 0x0C010C00u);
+    e[q] = as_u32((as_h2(and_or(d, 0x000F000Fu, c64)) - as_h2(zE)) * as_h2(sE));
+    o[q] = as_u32((as_h2(and_or(d, 0x00F000F0u, c54)) - as_h2(zO)) * as_h2(sO));
+  };
+
+  // vmcnt(n) with lgkmcnt(0) (vmcnt is split: bits 3:0 and 15:14)
+  constexpr int VM1 = DMA_PER_STEP, VM2 = 2 * DMA_PER_STEP;
+  constexpr int WAIT_BAR = (VM1 & 15) | ((VM1 >> 4) << 14) | (7 << 4) | (0 << 8);
+  constexpr int WAIT_PRO = (VM2 & 15) | ((VM2 >> 4) << 14) | (7 << 4) | (0 << 8);
+  // The barrier: the compiler may not move LDS accesses across it (the empty
+  // asm is a compiler memory barrier); no wait beyond the explicit one.
+  auto barrier = [&]() __attribute__((always_inline)) {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  // prologue: steps 0, 1 and 2 in flight, step 0 landed, slice 0 read
+  issue(0, 0);
+  issue(1, 1);
+  issue(2, 2);
+  __builtin_amdgcn_s_waitcnt(WAIT_PRO);
+  barrier();
+  load_scales(0);
+  {
+    const v2i x = read_w(0, 0);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) read_a(0, 0, 0, mb);
+    u32x4 e, o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dequant_pair(x, 0, q, e, o);
+    wf[0][0] = __builtin_bit_cast(h8, e);
+    wf[0][1] = __builtin_bit_cast(h8, o);
+  }
+
+  // One k16 slice: 8 MFMAs on buffer `cur`; the next slice (nst, cn) read
+  // into the other buffer while they run: the byte column first, the A
+  // fragments next, the dequantisation last (its bytes have landed by then).
+  // (After the last step the reads go to a stage that is not used again.)
+  auto slice = [&](int cur, int nst, int cn, auto body) __attribute__((always_inline)) {
+    v2i x;
+    u32x4 e, o;
+#pragma unroll
+    for (int q = 0; q < 2 * MB; ++q) {
+      const int mb = q >> 1, nb = q & 1;
+      acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[cur][nb], fa[cur][mb], acc[mb][nb], 0, 0, 0);
+      if (q == 0) x = read_w(nst, cn);
+      if (q >= 1 && q < MB + 1) read_a(nst, cn, cur ^ 1, q - 1);
+      if (q >= MB - 1 && q < MB + 3) dequant_pair(x, cur ^ 1, q - (MB - 1), e, o);
+      body(q);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    wf[cur ^ 1][0] = __builtin_bit_cast(h8, e);
+    wf[cur ^ 1][1] = __builtin_bit_cast(h8, o);
+  };
+  auto none = [](int) {};
+
+  // Step kt on stage ST = kt % 3 (a compile-time constant in each unrolled copy).
+  auto step = [&](int kt, auto stc) __attribute__((always_inline)) {
+    constexpr int ST = decltype(stc)::value;
+    constexpr int NST = (ST + 1) % 3;
+    slice(0, ST, 1, none);
+    slice(1, ST, 2, none);
+    slice(0, ST, 3, none);
+    // step kt + 1 landed (each wavefront waits for its own DMA, only step
+    // kt + 2's may still be in flight; the barrier publishes all of them) and
+    // every wavefront has its stage-ST fragments in registers
+    __builtin_amdgcn_s_waitcnt(WAIT_BAR);
+    barrier();
+    load_scales(NST);
+    slice(1, NST, 0, [&](int q) {
+      issue_one(kt + 3, ST, q);
+      if (q == 2 * MB - 1) {
+#pragma unroll
+        for (int d = 2 * MB; d < DMA_PER_STEP; ++d) issue_one(kt + 3, ST, d);
+      }
+    });
+  };
+  int kt = 0;
+  for (; kt + 2 < nk; kt += 3) {
+    step(kt, std::integral_constant<int, 0>{});
+    step(kt + 1, std::integral_constant<int, 1>{});
+    step(kt + 2, std::integral_constant<int, 2>{});
+  }
+  if (kt < nk) step(kt, std::integral_constant<int, 0>{});
+  if (kt + 1 < nk) step(kt + 1, std::integral_constant<int, 1>{});
+  __builtin_amdgcn_s_waitcnt(0);
+
+  // Epilogue: element 4g + e of accumulator (mb, nb) is row 32 (MB wm + mb) + j,
+  // column 64 wn + 16 g + 8 h + 2 e + nb of the tile.
+  const int col0 = tile.n0 + 64 * wn + 8 * h;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int m = tile.m0 + 32 * (MB * wm + mb) + j;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int n = col0 + 16 * g;
+      u32x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[e] = as_u32(f16x2{(_Float16)acc[mb][0][4 * g + e], (_Float16)acc[mb][1][4 * g + e]});
+      if (m < M && n < N) *reinterpret_cast<u32x4*>(Y + (int64_t)m * N + n) = v;
+    }
+  }
+}
+}  // namespace p8
+
+// Blocks [0, n_full) take 256-row tiles of columns [0, 256 n_split); blocks
+// n_full .. take 192-row tiles of the remaining columns.  Each part is
+// numbered XCD-aware on its own (both start at a multiple of 8 blocks).
+__global__ void __launch_bounds__(p8::THREADS, 1)
+    w4a16_prefill(const _Float16* __restrict__ A, const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
+                   const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int M, int N, int K, int group,
+                   int tiles_m, int n_split, int n_full, int tail_m, int tail_n, int tail_blocks) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 lds_h[];
+  uint8_t* const lds = reinterpret_cast<uint8_t*>(lds_h);
+  const int b = blockIdx.x;
+  if (b < n_full) {
+    p8::tile8<4>(lds, A, W, S, Z, Y, M, N, K, group, p8::tile_of(b, n_full, tiles_m, n_split, 256, 0));
+  } else {
+    const int tb = b - n_full;
+    const int n_tail = tail_m * tail_n;
+    const int idx = p8::remap_xcd(tb, tail_blocks);
+    if (idx >= n_tail) return;
+    p8::tile8<3>(lds, A, W, S, Z, Y, M, N, K, group, p8::tile_in_grid(idx, tail_m, tail_n, 192, n_split * BN));
+  }
+}
+
 }  // namespace w4a16
 }  // namespace tb
 
@@ -972,6 +1338,51 @@ static tb_status check_dense_args(const char* fn, const uint16_t* A, const uint8
 // Launch of the dense W4A16 GEMM after the checks: the split-K decode kernel
 // for M <= 16 (counters at `workspace`, fp32 partials DEC_COUNTER_BYTES past
 // it), the MFMA prefill kernel otherwise.
+// How the dense prefill covers the output: 256-row tiles over the first
+// n_split tile columns, then 192-row tiles over the rest, chosen so that the
+// work splits into whole rounds of one tile per CU as evenly as it can
+// (a 192-row tile costs about TAIL_COST of a 256-row one).
+struct PrefillPlan {
+  int n_split, n_full, tail_m, tail_n, tail_blocks;
+};
+// measured on MI355X: a round of 192-row tiles takes 0.86 of a round of 256-row ones
+constexpr double TAIL_COST = 0.86;
+static PrefillPlan plan_prefill(int M, int tiles_m, int tiles_n, int cus) {
+  auto makespan = [&](int full, int tail) {
+    // greedy list schedule of `full` unit jobs then `tail` TAIL_COST jobs on `cus` CUs
+    const double rounds_full = (double)(full / cus);
+    const int rem = full % cus;
+    // CUs with rounds_full + 1 full jobs: rem; the tail jobs go to the idle ones first
+    std::vector<double> load((size_t)cus, rounds_full);
+    for (int i = 0; i < rem; ++i) load[(size_t)i] += 1.0;
+    std::make_heap(load.begin(), load.end(), std::greater<double>());
+    for (int i = 0; i < tail; ++i) {
+      std::pop_heap(load.begin(), load.end(), std::greater<double>());
+      load.back() += TAIL_COST;
+      std::push_heap(load.begin(), load.end(), std::greater<double>());
+    }
+    return *std::max_element(load.begin(), load.end());
+  };
+  PrefillPlan p{tiles_n, tiles_m * tiles_n, 0, 0, 0};
+  const int tail_m = (M + 191) / 192;
+  double best = makespan(tiles_m * tiles_n, 0);
+  for (int s = tiles_n - 1; s >= 0; --s) {
+    if ((tiles_m * s) % 8 != 0) continue;
+    const double t = makespan(tiles_m * s, tail_m * (tiles_n - s));
+    if (t < best * 0.97) {
+      best = t;
+      p.n_split = s;
+    }
+  }
+  if (p.n_split < tiles_n) {
+    p.n_full = tiles_m * p.n_split;
+    p.tail_m = tail_m;
+    p.tail_n = tiles_n - p.n_split;
+    p.tail_blocks = (tail_m * p.tail_n + 7) / 8 * 8;
+  }
+  return p;
+}
+
 static tb_status launch_dense(const char* fn, const uint16_t* A, const uint8_t* W, const uint16_t* scales,
                               const uint8_t* zeros, uint16_t* Y, int64_t M, int64_t N, int64_t K, int64_t group,
                               void* workspace, hipStream_t stream) {
@@ -991,11 +1402,13 @@ static tb_status launch_dense(const char* fn, const uint16_t* A, const uint8_t* 
                          reinterpret_cast<_Float16*>(Y), partials, counters, (int)M, (int)N, (int)K, (int)group, splits);
     return tb::launch_status(fn);
   }
-  if (tb_status st = tb::reserve_lds(reinterpret_cast<const void*>(&w4a16_prefill), LDS4_BYTES, fn)) return st;
+  if (tb_status st = tb::reserve_lds(reinterpret_cast<const void*>(&w4a16_prefill), p8::LDS_BYTES, fn)) return st;
   const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
-  hipLaunchKernelGGL(w4a16_prefill, dim3(tiles_m * tiles_n), dim3(T4), LDS4_BYTES, stream,
+  const PrefillPlan pl = plan_prefill((int)M, tiles_m, tiles_n, device_cus());
+  hipLaunchKernelGGL(w4a16_prefill, dim3(pl.n_full + pl.tail_blocks), dim3(p8::THREADS), p8::LDS_BYTES, stream,
                      reinterpret_cast<const _Float16*>(A), W, reinterpret_cast<const _Float16*>(scales), zeros,
-                     reinterpret_cast<_Float16*>(Y), (int)M, (int)N, (int)K, (int)group, tiles_m, tiles_n);
+                     reinterpret_cast<_Float16*>(Y), (int)M, (int)N, (int)K, (int)group, tiles_m, pl.n_split,
+                     pl.n_full, pl.tail_m, pl.tail_n, pl.tail_blocks);
   return tb::launch_status(fn);
 }
 
