@@ -17,13 +17,18 @@
 //   3. the lane's candidates, elements >= T (float compare: -0 == +0), as a
 //      bit mask built with one compare and one add-with-carry per element;
 //   4. the row's candidates are compacted (prefix sum of the lane counts) into
-//      an LDS list of row indices; with at most 16 of them, lane i takes
-//      candidate i as the exact (key, 1023 - index) pair and a bitonic network
-//      over the 16 lanes sorts them: lane t ends with the t-th selection.
+//      an LDS list of exact (key, 1023 - index) pairs; with at most 16 of
+//      them, lane i takes candidate i and a bitonic network over the 16 lanes
+//      sorts them: lane t ends with the t-th selection.  With 17 to 32, lane i
+//      also takes candidate i + 16, both lists are sorted and merged (lane t
+//      keeps the larger of list 0's t-th and list 1's (15 - t)-th, a bitonic
+//      sequence holding the top 16, sorted by four half-cleaners).
 // On random logits a row has about 10 candidates at k = 8; 2.6 % of the
-// wavefronts at E = 256 (0.2 % at E = 64) have a row with more than 16.  A
-// wavefront any of whose rows has more than 16, or holds inf or NaN, runs the
-// exact path below on the staged rows instead (same results, more work).
+// wavefronts at E = 256 (0.2 % at E = 64) have a row with more than 16, and
+// far fewer one with more than 32.  A wavefront any of whose rows has more
+// than 32, or holds inf or NaN, runs the exact path below instead (same
+// results, more work); with one load per lane (E = 64 in fp32) the lanes
+// already hold the exact path's layout, otherwise the row is staged in LDS.
 //
 // exact path (every other shape, and the fallback).  A row is owned by LPR
 // consecutive lanes (a power of two), lane q holding elements q*V .. q*V+V-1
@@ -367,6 +372,7 @@ __device__ __forceinline__ uint32_t partner16(uint32_t v) {
   if constexpr (KIND == 3) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x1B, 0xF, 0xF, false);
   if constexpr (KIND == 4) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false);
   if constexpr (KIND == 5) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false);
+  if constexpr (KIND == 6) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);  // row_ror:8
 }
 
 template <int KIND, int BIT>
@@ -426,8 +432,11 @@ __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__
   constexpr int ROWS = kBlock / LPR;
   static_assert(CB == 8 || CB == 16, "filter_kernel: 8- or 16-byte loads");
 
-  __shared__ __attribute__((aligned(16))) uint32_t stage[ROWS][ROWB / 4];
-  __shared__ uint16_t cand[ROWS][LPR];
+  // With one load per lane (NC == 1) lane q already holds elements q*V ..
+  // q*V + V - 1, the exact path's layout, so the row is not staged.
+  constexpr bool STAGED = NC > 1;
+  __shared__ __attribute__((aligned(16))) uint32_t stage[STAGED ? ROWS : 1][ROWB / 4];
+  __shared__ uint64_t cand[ROWS][2 * LPR];
 
   const int slot = threadIdx.x / LPR;
   const int q = threadIdx.x % LPR;
@@ -444,12 +453,12 @@ __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__
       const int off = c * LPR * CB + q * CB;
       if constexpr (CB == 16) {
         const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rowp + off));
-        *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(stage[slot]) + off) = x;
+        if constexpr (STAGED) *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(stage[slot]) + off) = x;
 #pragma unroll
         for (int i = 0; i < 4; ++i) w[c * 4 + i] = x[i];
       } else {
         const u32x2 x = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(rowp + off));
-        *reinterpret_cast<u32x2*>(reinterpret_cast<char*>(stage[slot]) + off) = x;
+        if constexpr (STAGED) *reinterpret_cast<u32x2*>(reinterpret_cast<char*>(stage[slot]) + off) = x;
 #pragma unroll
         for (int i = 0; i < 2; ++i) w[c * 2 + i] = x[i];
       }
@@ -489,16 +498,26 @@ __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__
   incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, true);  // row_shr:8
   const int total = __shfl(incl, LPR - 1, LPR);
 
-  if (__builtin_amdgcn_ballot_w64(!(finite && total <= LPR)) == 0) {
-    // 4. compact the row's candidates (row indices) into cand[slot]
-    uint32_t mm = mask;
+  if (__builtin_amdgcn_ballot_w64(!(finite && total <= 2 * LPR)) == 0) {
+    // 4. compact the row's candidates into cand[slot], each as the exact
+    // (key, 1023 - index) pair, so a lane reads its candidate in one step
     int pos = incl - cnt;
-    while (__builtin_amdgcn_ballot_w64(mm != 0)) {
-      if (mm != 0) {
-        const int j = __builtin_ctz(mm);
-        mm &= mm - 1;
-        const int idx = (j / EPC) * (LPR * EPC) + q * EPC + (j % EPC);
-        cand[slot][pos++] = (uint16_t)idx;
+    auto put = [&](int j) {
+      const int idx = (j / EPC) * (LPR * EPC) + q * EPC + (j % EPC);
+      cand[slot][pos++] = ((uint64_t)key_of_bits(f[j]) << 32) | (uint32_t)(1023 - idx);
+    };
+    if constexpr (V <= 4) {
+#pragma unroll
+      for (int j = 0; j < V; ++j)
+        if ((mask >> j) & 1u) put(j);
+    } else {
+      uint32_t mm = mask;
+      while (__builtin_amdgcn_ballot_w64(mm != 0)) {
+        if (mm != 0) {
+          const int j = __builtin_ctz(mm);
+          mm &= mm - 1;
+          put(j);
+        }
       }
     }
     // The list is read by other lanes of this wavefront only (each wavefront
@@ -507,15 +526,26 @@ __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // lane q takes candidate q as (key, 1023 - index); 0 marks no candidate
-    uint64_t v = 0;
-    if (q < total) {
-      const int idx = cand[slot][q];
-      const uint32_t word = stage[slot][idx * ESZ / 4];
-      const uint32_t key = key_of_bits(f32_bits<DT>(word, idx & 1));
-      v = ((uint64_t)key << 32) | (uint32_t)(1023 - idx);
+    // lane q takes candidate q; 0 marks no candidate
+    uint64_t v = q < total ? cand[slot][q] : 0;
+    if (__builtin_amdgcn_ballot_w64(total > LPR) == 0) {
+      v = sort16_desc(v, q);
+    } else {
+      // a row of this wavefront has 17..32 candidates: lane q also takes
+      // candidate q + 16, both lists are sorted, and lane t keeps the larger
+      // of v[t] and v1[15 - t]; those 16 are the top 16 of the union as a
+      // bitonic sequence, which the half-cleaners at distances 8, 4, 2, 1 sort
+      uint64_t v1 = q + LPR < total ? cand[slot][q + LPR] : 0;
+      v = sort16_desc(v, q);
+      v1 = sort16_desc(v1, q);
+      const u32x2 b = __builtin_bit_cast(u32x2, v1);
+      const uint64_t m = __builtin_bit_cast(uint64_t, u32x2{partner16<5>(b.x), partner16<5>(b.y)});
+      v = v > m ? v : m;
+      v = cx_u64<6, 8>(v, q);
+      v = cx_u64<2, 4>(v, q);
+      v = cx_u64<1, 2>(v, q);
+      v = cx_u64<0, 1>(v, q);
     }
-    v = sort16_desc(v, q);
 
     // lane t < k holds selection t
     const float val = float_of_key((uint32_t)(v >> 32));
@@ -538,7 +568,7 @@ __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const int idx = q * V + j;
-      u[j] = key_of_bits(f32_bits<DT>(stage[slot][idx * ESZ / 4], idx & 1));
+      u[j] = key_of_bits(STAGED ? f32_bits<DT>(stage[slot][idx * ESZ / 4], idx & 1) : f[j]);
     }
     double sel[KMAX];
     exact_select<V, LPR, KMAX>(u, q, sel);
