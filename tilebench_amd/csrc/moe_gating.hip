@@ -6,8 +6,7 @@
 // filter_kernel (E = 16·V with V in {4, 8, 16} and 2 < k <= 8: the BASELINE
 // shapes).  A row is owned by 16 lanes; each lane loads V logits
 // with 16-byte loads (8-byte when V·size < 16) laid out so that one load
-// instruction of the row's 16 lanes covers 256 contiguous bytes.  The row is
-// also staged in LDS as loaded.  Per lane:
+// instruction of the row's 16 lanes covers 256 contiguous bytes.  Per lane:
 //   1. the lane maximum m_q (signed-int order of the float bits, two VALU ops
 //      per element for the key, max3/min3 folds);
 //   2. T = the k-th largest of the 16 lane maxima (a bitonic network across
@@ -375,17 +374,57 @@ __device__ __forceinline__ uint32_t partner16(uint32_t v) {
   if constexpr (KIND == 6) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);  // row_ror:8
 }
 
+// Partner at distance 4 (lane p ^ 4) from two DPP row rotations, which stay
+// off the LDS crossbar: row_ror:n hands lane p the value of lane (p - n) % 16,
+// so lanes with bit 2 set read through row_ror:4, the others row_ror:12.
+__device__ __forceinline__ uint32_t xor4_16(uint32_t v, int p) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, false);  // row_ror:4: p - 4
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x12C, 0xF, 0xF, false);  // row_ror:12: p + 4
+  return (p & 4) ? lo : hi;
+}
+template <int KIND>
+__device__ __forceinline__ uint32_t partner16p(uint32_t v, int p) {
+  if constexpr (KIND == 2) return xor4_16(v, p);
+  return partner16<KIND>(v);
+}
 template <int KIND, int BIT>
 __device__ __forceinline__ int32_t cx_i32(int32_t v, int p) {
-  const int32_t w = (int32_t)partner16<KIND>((uint32_t)v);
+  const int32_t w = (int32_t)partner16p<KIND>((uint32_t)v, p);
   return (p & BIT) ? (v < w ? v : w) : (v > w ? v : w);
 }
 template <int KIND, int BIT>
 __device__ __forceinline__ uint64_t cx_u64(uint64_t v, int p) {
   const u32x2 b = __builtin_bit_cast(u32x2, v);
-  const u32x2 o = {partner16<KIND>(b.x), partner16<KIND>(b.y)};
+  const u32x2 o = {partner16p<KIND>(b.x, p), partner16p<KIND>(b.y, p)};
   const uint64_t w = __builtin_bit_cast(uint64_t, o);
   return ((v > w) == ((p & BIT) == 0)) ? v : w;
+}
+// Lane n of the caller's 16-lane row, broadcast to the row (DPP row_newbcast).
+template <int N>
+__device__ __forceinline__ uint32_t row_bcast(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x150 + N, 0xF, 0xF, false);
+}
+template <int N>
+__device__ __forceinline__ float row_bcast_f(float v) {
+  return __builtin_bit_cast(float, row_bcast<N>(__builtin_bit_cast(uint32_t, v)));
+}
+// e[t] = lane t's x, for every t of the sequence
+template <int... T, size_t N>
+__device__ __forceinline__ void bcast_all(float x, float (&e)[N], std::integer_sequence<int, T...>) {
+  ((e[T] = row_bcast_f<T>(x)), ...);
+}
+// Lane n (0 <= n < 8, wave-uniform) of the row, broadcast to the row.
+__device__ __forceinline__ uint32_t row_bcast_lt8(uint32_t v, int n) {
+  switch (n) {
+    case 0: return row_bcast<0>(v);
+    case 1: return row_bcast<1>(v);
+    case 2: return row_bcast<2>(v);
+    case 3: return row_bcast<3>(v);
+    case 4: return row_bcast<4>(v);
+    case 5: return row_bcast<5>(v);
+    case 6: return row_bcast<6>(v);
+    default: return row_bcast<7>(v);
+  }
 }
 
 // Descending sort of one value per lane across the 16 lanes of a row (p = lane
@@ -481,7 +520,7 @@ __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__
 
   // 2. T = the k-th largest lane maximum (flip order refines float order, so
   // the k lanes above it hold k elements that are >= T as floats)
-  const int32_t tkey = __shfl(sort16_desc(kmax, q), k - 1, LPR);
+  const int32_t tkey = (int32_t)row_bcast_lt8((uint32_t)sort16_desc(kmax, q), k - 1);  // k <= KMAX = 8
   const float T = __builtin_bit_cast(float, (uint32_t)flip_key((uint32_t)tkey));
 
   // 3. candidate mask, bit j for element j
@@ -496,7 +535,7 @@ __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__
   incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, true);  // row_shr:2
   incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, true);  // row_shr:4
   incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, true);  // row_shr:8
-  const int total = __shfl(incl, LPR - 1, LPR);
+  const int total = (int)row_bcast<LPR - 1>((uint32_t)incl);
 
   if (__builtin_amdgcn_ballot_w64(!(finite && total <= 2 * LPR)) == 0) {
     // 4. compact the row's candidates into cand[slot], each as the exact
@@ -549,11 +588,10 @@ __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__
 
     // lane t < k holds selection t
     const float val = float_of_key((uint32_t)(v >> 32));
-    const float v0 = __shfl(val, 0, LPR);
+    const float v0 = row_bcast_f<0>(val);
     const float et = q < k ? expf(val - v0) : 0.f;
     float e[KMAX];
-#pragma unroll
-    for (int t = 0; t < KMAX; ++t) e[t] = __shfl(et, t, LPR);
+    bcast_all(et, e, std::make_integer_sequence<int, KMAX>{});
     const float sum = np_sum<KMAX>(e, k);
     if (q < k) {
       store_weight<DT>(weights, r * k + q, et / sum);
