@@ -27,7 +27,7 @@
 // far fewer one with more than 32.  A wavefront any of whose rows has more
 // than 32, or holds inf or NaN, runs the exact path below instead (same
 // results, more work); with one load per lane (E = 64 in fp32) the lanes
-// already hold the exact path's layout, otherwise the row is staged in LDS.
+// already hold the exact path's layout, otherwise they read it again.
 //
 // exact path (every other shape, and the fallback).  A row is owned by LPR
 // consecutive lanes (a power of two), lane q holding elements q*V .. q*V+V-1
@@ -471,10 +471,6 @@ __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__
   constexpr int ROWS = kBlock / LPR;
   static_assert(CB == 8 || CB == 16, "filter_kernel: 8- or 16-byte loads");
 
-  // With one load per lane (NC == 1) lane q already holds elements q*V ..
-  // q*V + V - 1, the exact path's layout, so the row is not staged.
-  constexpr bool STAGED = NC > 1;
-  __shared__ __attribute__((aligned(16))) uint32_t stage[STAGED ? ROWS : 1][ROWB / 4];
   __shared__ uint64_t cand[ROWS][2 * LPR];
 
   const int slot = threadIdx.x / LPR;
@@ -492,12 +488,10 @@ __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__
       const int off = c * LPR * CB + q * CB;
       if constexpr (CB == 16) {
         const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rowp + off));
-        if constexpr (STAGED) *reinterpret_cast<u32x4*>(reinterpret_cast<char*>(stage[slot]) + off) = x;
 #pragma unroll
         for (int i = 0; i < 4; ++i) w[c * 4 + i] = x[i];
       } else {
         const u32x2 x = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(rowp + off));
-        if constexpr (STAGED) *reinterpret_cast<u32x2*>(reinterpret_cast<char*>(stage[slot]) + off) = x;
 #pragma unroll
         for (int i = 0; i < 2; ++i) w[c * 2 + i] = x[i];
       }
@@ -598,15 +592,25 @@ __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__
       indices[r * k + q] = 1023 - (int)(uint32_t)v;
     }
   } else {
-    // exact path on the staged rows: lane q takes elements q*V .. q*V+V-1
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // exact path: lane q takes elements q*V .. q*V+V-1.  With one load per
+    // lane it already holds them; otherwise it reads them again (this path is
+    // rare) rather than staging every row in LDS.
     uint32_t u[V];
+    if constexpr (NC == 1) {
 #pragma unroll
-    for (int j = 0; j < V; ++j) {
-      const int idx = q * V + j;
-      u[j] = key_of_bits(STAGED ? f32_bits<DT>(stage[slot][idx * ESZ / 4], idx & 1) : f[j]);
+      for (int j = 0; j < V; ++j) u[j] = key_of_bits(f[j]);
+    } else {
+      const uint32_t* rw = reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(logits) + r * ROWB) +
+                           q * V * ESZ / 4;
+      uint32_t x[V * ESZ / 4];
+#pragma unroll
+      for (int c = 0; c < V * ESZ / 16; ++c) {
+        const u32x4 t = *reinterpret_cast<const u32x4*>(rw + 4 * c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[4 * c + i] = t[i];
+      }
+#pragma unroll
+      for (int j = 0; j < V; ++j) u[j] = key_of_bits(f32_bits<DT>(x[j * ESZ / 4], j & 1));
     }
     double sel[KMAX];
     exact_select<V, LPR, KMAX>(u, q, sel);
