@@ -1111,12 +1111,16 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
     }
   // Transposing byte read of slice c: lane p = 2r + b of its group of 16
   // (group G = lane / 16: columns 16 (G & 1) .., rows 8 (G >> 1) ..) points at
-  // row 16c + 8 (G >> 1) + r, bytes 32 wn + 16 (G & 1) + 8b .. +7.
+  // row 16c + 8 (G >> 1) + pi(r), bytes 32 wn + 16 (G & 1) + 8b .. +7, where
+  // pi swaps 1 <-> 2 and 5 <-> 6: byte r of the result then holds row pi(r),
+  // so each dword reads rows (0, 2, 1, 3) and a k-row pair sits in bytes 0 and
+  // 2 (or, shifted down by 8, in bytes 1 and 3) with no byte permute.
   uint32_t wt_off;
   {
     const int p = lane & 15, r = p >> 1, b = p & 1, G = lane >> 4;
+    const int pr = (r & 4) | ((r & 1) << 1) | ((r >> 1) & 1);
     const int cb = 2 * wn + (G & 1);
-    wt_off = (uint32_t)(A_ST + (8 * (G >> 1) + r) * 128 + ((cb ^ r) << 4) + 8 * b);
+    wt_off = (uint32_t)(A_ST + (8 * (G >> 1) + pr) * 128 + ((cb ^ pr) << 4) + 8 * b);
   }
 
   f32x16 acc[MB][2];
@@ -1152,12 +1156,12 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
     return __builtin_amdgcn_ds_read_tr8_b64_v2i32(
         (__attribute__((address_space(3))) v2i*)(base + st * STAGE + c * 2048 + wt_off));
   };
-  // k-row pairs (2q, 2q + 1) as {byte 2q, 0, byte 2q + 1, 0}; the even
-  // column's nibbles under 0x64 read 1024 + q, the odd column's (bits 7:4)
-  // under 0x54 read 64 + q.
+  // k-row pair (2q, 2q + 1) in bytes 0 and 2 of a word; the even column's
+  // nibbles under 0x64 read 1024 + q, the odd column's (bits 7:4) under 0x54
+  // read 64 + q (the masks ignore bytes 1 and 3).
   auto dequant_pair = [&](const v2i x, int buf, int q, u32x4& e, u32x4& o) __attribute__((always_inline)) {
     const uint32_t src = (uint32_t)x[q >> 1];
-    const uint32_t d = perm(src, src, (q & 1) ? 0x0C030C02u : 0x0C010C00u);
+    const uint32_t d = (q & 1) ? src >> 8 : src;  // k rows 2q, 2q + 1 in bytes 0 and 2
     e[q] = as_u32((as_h2(and_or(d, 0x000F000Fu, c64)) - as_h2(zE)) * as_h2(sE));
     o[q] = as_u32((as_h2(and_or(d, 0x00F000F0u, c54)) - as_h2(zO)) * as_h2(sO));
   };
