@@ -1185,31 +1185,35 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
   __builtin_amdgcn_s_waitcnt(WAIT_PRO);
   barrier();
   load_scales(0);
+  v2i xs[4];
   {
-    const v2i x = read_w(0, 0);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) xs[c] = read_w(0, c);
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) read_a(0, 0, 0, mb);
     u32x4 e, o;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dequant_pair(x, 0, q, e, o);
+    for (int q = 0; q < 4; ++q) dequant_pair(xs[0], 0, q, e, o);
     wf[0][0] = __builtin_bit_cast(h8, e);
     wf[0][1] = __builtin_bit_cast(h8, o);
   }
 
   // One k16 slice: 8 MFMAs on buffer `cur`; the next slice (nst, cn) read
-  // into the other buffer while they run: the byte column first, the A
-  // fragments next, the dequantisation last (its bytes have landed by then).
+  // into the other buffer while they run: its A fragments, then its
+  // dequantisation from the byte column xs[cn].  The slice after each
+  // barrier (cn == 0) also reads the byte columns of all four slices of the
+  // new stage, slice 0's first, so later slices never wait on them.
   // (After the last step the reads go to a stage that is not used again.)
   auto slice = [&](int cur, int nst, int cn, auto body) __attribute__((always_inline)) {
-    v2i x;
     u32x4 e, o;
 #pragma unroll
     for (int q = 0; q < 2 * MB; ++q) {
       const int mb = q >> 1, nb = q & 1;
       acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[cur][nb], fa[cur][mb], acc[mb][nb], 0, 0, 0);
-      if (q == 0) x = read_w(nst, cn);
+      if (cn == 0 && q == 0) xs[0] = read_w(nst, 0);
       if (q >= 1 && q < MB + 1) read_a(nst, cn, cur ^ 1, q - 1);
-      if (q >= MB - 1 && q < MB + 3) dequant_pair(x, cur ^ 1, q - (MB - 1), e, o);
+      if (cn == 0 && q >= 2 * MB - 3) xs[q - 2 * MB + 4] = read_w(nst, q - 2 * MB + 4);
+      if (q >= MB - 1 && q < MB + 3) dequant_pair(xs[cn], cur ^ 1, q - (MB - 1), e, o);
       body(q);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1224,12 +1228,18 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
     constexpr int NST = (ST + 1) % 3;
     slice(0, ST, 1, none);
     slice(1, ST, 2, none);
+    if (wm) __builtin_amdgcn_s_setprio(0);
     slice(0, ST, 3, none);
     // step kt + 1 landed (each wavefront waits for its own DMA, only step
     // kt + 2's may still be in flight; the barrier publishes all of them) and
     // every wavefront has its stage-ST fragments in registers
     __builtin_amdgcn_s_waitcnt(WAIT_BAR);
     barrier();
+    // The two wavefronts of a SIMD (w, w + 4) share its issue; by age the
+    // older one would run ahead and wait at the barrier while the younger
+    // finishes alone.  The younger one leads the three slices after each
+    // barrier, the older one the last, so both arrive together.
+    if (wm) __builtin_amdgcn_s_setprio(1);
     load_scales(NST);
     slice(1, NST, 0, [&](int q) {
       issue_one(kt + 3, ST, q);
