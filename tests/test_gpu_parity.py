@@ -421,6 +421,45 @@ def test_fp8_gemm_full_size_rows(gpu):
     np.testing.assert_allclose(Y[rows], ref, atol=1e-2, rtol=1e-2)
 
 
+def test_fp8_gemm_rounding_ties_and_specials(gpu):
+    """The epilogue's bf16 rounding and special values, on exact sums.
+
+    Sums of 1 and e4m3 subnormals land exactly on bf16 rounding ties (1 + 2^-8
+    rounds to 1, 1 + 3 * 2^-8 to 1 + 2^-6: to even) and next to them (1 + 5 *
+    2^-9 rounds up), in both signs; an e4m3 NaN code poisons its row; an
+    infinite column scale gives +-inf, or NaN where the sum is zero.  With unit
+    scales the oracle's value is exact, so finite outputs must match it bit for
+    bit and NaNs position for position."""
+    from tilebench_amd.benchmarks.operators.fp8_scaled_gemm import impl_hip
+
+    M, N, K = 64, 64, 128
+    _say("fp8_scaled_gemm specials", M, N, K)
+    A = np.zeros((M, K), np.uint8)
+    W = np.zeros((K, N), np.uint8)
+    A[0, 0] = A[0, 1] = 0x38            # +1, +1
+    A[1, 0] = A[1, 1] = 0xB8            # -1, -1
+    A[2, 0], A[2, 1] = 0x7F, 0x38       # NaN poisons row 2
+    A[4, 0] = 0x38                      # row 4: exactly 1 (+ W[1, n] * 0)
+    W[0, :] = 0x38                      # 1.0 in every column
+    W[1, 0], W[1, 1], W[1, 2] = 0x02, 0x06, 0x05  # 2^-8, 3 * 2^-8, 5 * 2^-9
+    sa = np.ones(M, np.float32)
+    sw = np.ones(N, np.float32)
+    sw[5] = np.inf
+    to_t = lambda x: torch.from_numpy(x).view(torch.float8_e4m3fn)
+    Y = impl_hip.run(to_t(A).to(gpu), to_t(W).to(gpu), torch.from_numpy(sa).to(gpu), torch.from_numpy(sw).to(gpu))
+    torch.cuda.synchronize()
+    got = Y.view(torch.int16).cpu().numpy().view(np.uint16)
+    with np.errstate(invalid="ignore"):  # 0 * inf in column 5 is the NaN being tested
+        ref = oracle.fp8_scaled_gemm(A, W, sa, sw)
+    gotf, reff = oracle.bf16_bits_to_f32(got), oracle.bf16_bits_to_f32(ref)
+    assert np.array_equal(np.isnan(gotf), np.isnan(reff))
+    fin = ~np.isnan(reff)
+    assert np.array_equal(got[fin], ref[fin])
+    assert got[0, 0] == 0x3F80 and got[0, 1] == 0x3F82 and got[0, 2] == 0x3F81
+    assert got[1, 0] == 0xBF80 and got[1, 1] == 0xBF82 and got[1, 2] == 0xBF81
+    assert np.isnan(gotf[2]).all() and np.isnan(gotf[3, 5]) and gotf[0, 5] == np.inf and gotf[1, 5] == -np.inf
+
+
 def test_golden_fixtures_on_gpu(gpu):
     """Every committed golden fixture reproduced by the GPU kernels."""
     import os

@@ -43,21 +43,17 @@ typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 constexpr int BM = 256, BN = 256, BK = 128, THREADS = 256, GROUP_M = 8;
 constexpr int STAGE = BM * BK;  // bytes per operand stage
 constexpr int C_STRIDE = BN + 8;  // bf16 elements per staged output row (16-byte pad)
-// A and B, two stages each (128 KiB), reused for the staged bf16 output tile.
-constexpr size_t LDS_BYTES = 4 * (size_t)STAGE > (size_t)BM * C_STRIDE * 2 ? 4 * (size_t)STAGE
-                                                                           : (size_t)BM * C_STRIDE * 2;
+// A and B, two stages each (128 KiB), reused for the staged bf16 output tile,
+// then the tile's row and column scales (1 KiB each), loaded at the start.
+constexpr size_t TILE_BYTES = 4 * (size_t)STAGE > (size_t)BM * C_STRIDE * 2 ? 4 * (size_t)STAGE
+                                                                            : (size_t)BM * C_STRIDE * 2;
+constexpr size_t SA_OFF = TILE_BYTES, SW_OFF = TILE_BYTES + BM * 4;
+constexpr size_t LDS_BYTES = SW_OFF + BN * 4;
+static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 constexpr uint32_t RSRC_DW3 = 0x00020000u;
 constexpr uint32_t OOB = 0x80000000u;
 
 __device__ __forceinline__ int slot(int row, int chunk) { return row * BK + ((chunk ^ ((row ^ (row >> 3)) & 7)) << 4); }
-
-// fp32 -> bf16 bits, round to nearest even, NaN kept quiet; a select, not a
-// branch, so the epilogue's 256 conversions per lane stay straight-line code.
-__device__ __forceinline__ uint32_t bf16_rne_sel(float f) {
-  const uint32_t b = __builtin_bit_cast(uint32_t, f);
-  const uint32_t r = (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
-  return (b & 0x7FFFFFFFu) > 0x7F800000u ? ((b >> 16) | 0x40u) : r;
-}
 
 struct Tile {
   int m0, n0;
@@ -100,6 +96,15 @@ __device__ __forceinline__ void dma16(uint32_t lds_addr, uint32_t voff, const i3
                : "memory", "m0");
 }
 
+// One 4-byte-per-lane DMA into LDS at m0 (lane l -> +4 l).
+__device__ __forceinline__ void dma4(uint32_t lds_addr, uint32_t voff, const i32x4& rsrc, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane((int)lds_addr)), "v"(voff), "s"(rsrc),
+                 "s"(__builtin_amdgcn_readfirstlane((int)soff))
+               : "memory", "m0");
+}
+
 __global__ void __launch_bounds__(THREADS, 1)
     fp8_gemm_kernel(const uint8_t* __restrict__ Aq, const uint8_t* __restrict__ WqT, const float* __restrict__ sa,
                     const float* __restrict__ sw, uint16_t* __restrict__ Y, int M, int N, int K, int tiles_m,
@@ -111,6 +116,9 @@ __global__ void __launch_bounds__(THREADS, 1)
 
   const i32x4 ra = make_rsrc4(Aq, (uint32_t)M * (uint32_t)K);
   const i32x4 rb = make_rsrc4(WqT, (uint32_t)N * (uint32_t)K);
+  // the DMAs issued past the last step read through empty resources: zeros,
+  // no memory traffic, nothing for the epilogue to wait on
+  const i32x4 ra0 = make_rsrc4(Aq, 0u), rb0 = make_rsrc4(WqT, 0u);
   // DMA: per operand and stage, 32 instructions of 1 KiB (8 rows); wave w issues 8 of each.
   uint32_t a_off[8], b_off[8];
   {
@@ -128,13 +136,15 @@ __global__ void __launch_bounds__(THREADS, 1)
       (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
   // LDS layout [A stage 0 | A stage 1 | B stage 0 | B stage 1], 32 KiB each.
   // DMA instruction q (0..15) of step kt: A rows for q < 8, B rows for q >= 8.
+  const int nk = K / BK;
   auto dma = [&](int kt, int q) {
     const uint32_t st = lds0 + (uint32_t)((kt & 1) * STAGE) + (uint32_t)(wave * 8 * 1024);
     const uint32_t soff = (uint32_t)(kt * BK);
+    const bool live = kt < nk;
     if (q < 8)
-      dma16(st + q * 1024, a_off[q], ra, soff);
+      dma16(st + q * 1024, a_off[q], live ? ra : ra0, soff);
     else
-      dma16(st + 2 * STAGE + (q - 8) * 1024, b_off[q - 8], rb, soff);
+      dma16(st + 2 * STAGE + (q - 8) * 1024, b_off[q - 8], live ? rb : rb0, soff);
   };
 
   // Fragment f (0..3 A rows, 4..7 B rows) of substep s: row base + (f & 3) * 32
@@ -187,8 +197,15 @@ __global__ void __launch_bounds__(THREADS, 1)
 
   constexpr int WAIT_VM0 = 0 | (7 << 4) | (15 << 8);
   constexpr int WAIT_VM16_LGKM0 = 0 | (7 << 4) | (0 << 8) | (1 << 14);  // vmcnt(16), lgkmcnt(0)
-  const int nk = K / BK;
-  // Prologue: stages 0 and 1 in flight, wait for stage 0, read its substep-0 fragments.
+  // Prologue: the tile's scales (wave w: rows and columns 64w .. 64w + 63;
+  // zeros past M or N), then stages 0 and 1 in flight, wait for stage 0, read
+  // its substep-0 fragments.
+  {
+    const i32x4 rsa = make_rsrc4(sa, (uint32_t)M * 4u), rsw = make_rsrc4(sw, (uint32_t)N * 4u);
+    const int m = tile.m0 + wave * 64 + lane, n = tile.n0 + wave * 64 + lane;
+    dma4(lds0 + (uint32_t)(SA_OFF + wave * 256), m < M ? (uint32_t)m * 4u : OOB, rsa, 0u);
+    dma4(lds0 + (uint32_t)(SW_OFF + wave * 256), n < N ? (uint32_t)n * 4u : OOB, rsw, 0u);
+  }
 #pragma unroll
   for (int q = 0; q < 16; ++q) dma(0, q);
   if (nk > 1) {
@@ -242,24 +259,23 @@ __global__ void __launch_bounds__(THREADS, 1)
   // row i*32 + lane%32, column j*32 + (e/4)*8 + (lane/32)*4 + e%4 of the wave tile.
   __syncthreads();  // every wave is done with the stages before they hold the output tile
   uint16_t* ct = reinterpret_cast<uint16_t*>(lds);
-  const buf_rsrc_t rsa = buf_rsrc(sa, (uint32_t)M * 4u), rsw = buf_rsrc(sw, (uint32_t)N * 4u);
+  // scales from LDS (landed before the first K step's barrier)
+  const float* lsa = reinterpret_cast<const float*>(lds + SA_OFF);
+  const float* lsw = reinterpret_cast<const float*>(lds + SW_OFF);
   float sav[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = tile.m0 + wm * 128 + i * 32 + (lane & 31);
-    sav[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsa, m < M ? (uint32_t)m * 4u : OOB, 0, 0));
-  }
-  float swv[4][4][4];  // [j][g][e]: column j*32 + g*8 + (lane/32)*4 + e
+  for (int i = 0; i < 4; ++i) sav[i] = lsa[wm * 128 + i * 32 + (lane & 31)];
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
+  typedef float f32x2v __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+  f32x4v swv[4][4];  // [j][g]: columns j*32 + g*8 + (lane/32)*4 + 0..3
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int g = 0; g < 4; ++g)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int n = tile.n0 + wn * 128 + j * 32 + g * 8 + (lane >> 5) * 4 + e;
-        swv[j][g][e] =
-            __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsw, n < N ? (uint32_t)n * 4u : OOB, 0, 0));
-      }
+      swv[j][g] = *reinterpret_cast<const f32x4v*>(lsw + wn * 128 + j * 32 + g * 8 + (lane >> 5) * 4);
+  // (acc * sa) * sw in fp32, then one RNE rounding to bf16 by the hardware
+  // converter (v_cvt_pk_bf16_f32)
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -268,12 +284,12 @@ __global__ void __launch_bounds__(THREADS, 1)
       for (int g = 0; g < 4; ++g) {
         const int row = wm * 128 + i * 32 + (lane & 31);
         const int col = wn * 128 + j * 32 + g * 8 + (lane >> 5) * 4;
-        uint32_t h[4];
+        float f[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = bf16_rne_sel(acc[i][j][4 * g + e] * sav[i] * swv[j][g][e]);
+        for (int e = 0; e < 4; ++e) f[e] = acc[i][j][4 * g + e] * sav[i] * swv[j][g][e];
         u32x2v v;
-        v[0] = h[0] | (h[1] << 16);
-        v[1] = h[2] | (h[3] << 16);
+        v[0] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v{f[0], f[1]}), bf16x2v));
+        v[1] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v{f[2], f[3]}), bf16x2v));
         *reinterpret_cast<u32x2v*>(ct + row * C_STRIDE + col) = v;
       }
   __syncthreads();
