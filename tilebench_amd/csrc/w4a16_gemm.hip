@@ -31,10 +31,13 @@
 //           last round would be part-empty, the host may cover the last tile
 //           columns with 192-row tiles instead, so that the work splits into
 //           whole rounds more evenly.
+// The grouped GEMM (w4a16_grouped) runs the same tile on each expert's
+// operands; a last column tile of at most 128 columns runs it as 256 x 128
+// (the eight wavefronts as 4 row groups x 2 column groups).
 // Every output element sees the same MFMA operands, in the same K order, as
-// in prefill_tile below, so the two kernels give bit-identical results.
+// in prefill_tile below, so the kernels give bit-identical results.
 //
-// Grouped and MoE kernels (prefill_tile): one 256 x 256 output tile per
+// MoE layer kernels (prefill_tile): one 256 x 256 output tile per
 // 512-thread block, eight wavefronts (two per SIMD) each owning a 128 x 64
 // sub-tile (8 v_mfma_f32_32x32x16_f16 accumulators = 128 fp32 per lane), K
 // advanced 64 at a time:
@@ -571,32 +574,6 @@ __device__ __forceinline__ int grouped_block_id() {
   return bid;
 }
 
-// Grouped (MoE) variant: rows offsets[e] .. offsets[e+1] of A use expert e's
-// weights.  The grid is an upper bound (sum over experts of ceil(rows / 256)
-// <= R / 256 + E tile rows, times the N tiles); each block walks the E + 1
-// offsets to find its expert and tile row, and blocks past the last tile exit.
-// Tile ids are regrouped per XCD as in the dense kernel, so the blocks
-// resident on one XCD work on neighbouring tiles of the same expert.
-__global__ void __launch_bounds__(T4, 1)
-    w4a16_grouped(const _Float16* __restrict__ A, const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
-                  const uint8_t* __restrict__ Z, const int* __restrict__ offsets, _Float16* __restrict__ Y, int R,
-                  int experts, int N, int K, int group, int tiles_n) {
-  extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
-  const int bid = grouped_block_id();
-  const int mt = bid / tiles_n, nt = bid - mt * tiles_n;
-  int e = 0, m0 = 0, m_end = 0;
-  if (!grouped_tile(offsets, experts, R, mt, e, m0, m_end)) return;  // beyond the last tile: uniform
-  const int64_t wstride = (int64_t)K * (N / 2), sstride = (int64_t)(K / group) * N, zstride = (int64_t)(K / group) * (N / 2);
-  // A last column tile of at most 128 columns (N = 1408 is 5.5 tiles) takes
-  // the narrow form: half the MFMAs and half the dequantisation per thread.
-  if (N - nt * BN <= BN / 2)
-    prefill_tile<A_DIRECT, EPI_PLAIN, true>(lds, A, W + e * wstride, S + e * sstride, Z + e * zstride, Y, R, m0,
-                                            m_end, nt * BN, N, K, group);
-  else
-    prefill_tile<A_DIRECT, EPI_PLAIN>(lds, A, W + e * wstride, S + e * sstride, Z + e * zstride, Y, R, m0, m_end,
-                                      nt * BN, N, K, group);
-}
-
 // MoE gate/up projection: rows of the pair space (sorted by expert, offsets[e]
 // .. offsets[e+1] for expert e) gather their token's activation row X[ids[m] /
 // topk], multiply by expert e's W13 [K, 2I] and write fp16(silu(gate) * up),
@@ -1009,18 +986,22 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t c
   return r;
 }
 
-// One tile of 64 MB rows (MB = 4: 256, MB = 3: 192) x 256 columns at (m0, n0).
-template <int MB>
+// One tile at (m0, n0): the eight wavefronts as 8 / WN row groups of 32 MB
+// rows times WN column groups of 64 columns.  WN = 4: 256 columns and 64 MB
+// rows (MB = 4: 256, MB = 3: 192); WN = 2, MB = 2: 256 rows x 128 columns,
+// for a last column tile of at most 128 columns.
+template <int MB, int WN = 4>
 __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16* __restrict__ A,
                                       const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
                                       const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int M, int N, int K,
                                       int group, const Tile tile) {
-  constexpr int TM = 64 * MB;       // tile rows
-  constexpr int AI = MB;            // A DMA instructions per wavefront and step (8 rows each)
+  static_assert((WN == 4 && (MB == 3 || MB == 4)) || (WN == 2 && MB == 2), "tile8 shapes");
+  constexpr int TM = 32 * MB * (8 / WN);  // tile rows
+  constexpr int AI = TM / 64;             // A DMA instructions per wavefront and step (8 rows each)
   constexpr int DMA_PER_STEP = AI + 5;
   const int t = threadIdx.x, lane = t & 63, h = lane >> 5, j = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int wm = w >> 2, wn = w & 3;
+  const int wm = w / WN, wn = w % WN;
   const int nk = K / BK;
   const uint32_t half_n = (uint32_t)(N / 2);
 
@@ -1213,7 +1194,9 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
       if (cn == 0 && q == 0) xs[0] = read_w(nst, 0);
       if (q >= 1 && q < MB + 1) read_a(nst, cn, cur ^ 1, q - 1);
       if (cn == 0 && q >= 2 * MB - 3) xs[q - 2 * MB + 4] = read_w(nst, q - 2 * MB + 4);
-      if (q >= MB - 1 && q < MB + 3) dequant_pair(xs[cn], cur ^ 1, q - (MB - 1), e, o);
+#pragma unroll
+      for (int dq = 0; dq < 4; ++dq)
+        if (q == (MB >= 3 ? MB - 1 + dq : 1 + dq / 2)) dequant_pair(xs[cn], cur ^ 1, dq, e, o);
       body(q);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1228,7 +1211,7 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
     constexpr int NST = (ST + 1) % 3;
     slice(0, ST, 1, none);
     slice(1, ST, 2, none);
-    if (wm) __builtin_amdgcn_s_setprio(0);
+    if (w >= 4) __builtin_amdgcn_s_setprio(0);
     slice(0, ST, 3, none);
     // step kt + 1 landed (each wavefront waits for its own DMA, only step
     // kt + 2's may still be in flight; the barrier publishes all of them) and
@@ -1239,7 +1222,7 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
     // older one would run ahead and wait at the barrier while the younger
     // finishes alone.  The younger one leads the three slices after each
     // barrier, the older one the last, so both arrive together.
-    if (wm) __builtin_amdgcn_s_setprio(1);
+    if (w >= 4) __builtin_amdgcn_s_setprio(1);
     load_scales(NST);
     slice(1, NST, 0, [&](int q) {
       issue_one(kt + 3, ST, q);
@@ -1297,6 +1280,36 @@ __global__ void __launch_bounds__(p8::THREADS, 1)
     if (idx >= n_tail) return;
     p8::tile8<3>(lds, A, W, S, Z, Y, M, N, K, group, p8::tile_in_grid(idx, tail_m, tail_n, 192, n_split * BN));
   }
+}
+
+// Grouped (MoE) variant: rows offsets[e] .. offsets[e+1] of A use expert e's
+// weights.  The grid is an upper bound (sum over experts of ceil(rows / 256)
+// <= R / 256 + E tile rows, times the N tiles); each block walks the E + 1
+// offsets to find its expert and tile row, and blocks past the last tile exit.
+// Tile ids are regrouped per XCD as in the dense kernel, so the blocks
+// resident on one XCD work on neighbouring tiles of the same expert.  A tile
+// is the dense kernel's 256 x 256 tile on the expert's operands, its A and Y
+// based at the tile's first row with the rows up to the expert's last as the
+// valid ones, so each expert segment equals the dense product bit for bit.
+__global__ void __launch_bounds__(p8::THREADS, 1)
+    w4a16_grouped(const _Float16* __restrict__ A, const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
+                  const uint8_t* __restrict__ Z, const int* __restrict__ offsets, _Float16* __restrict__ Y, int R,
+                  int experts, int N, int K, int group, int tiles_n) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 lds_h[];
+  uint8_t* const lds = reinterpret_cast<uint8_t*>(lds_h);
+  const int bid = grouped_block_id();
+  const int mt = bid / tiles_n, nt = bid - mt * tiles_n;
+  int e = 0, m0 = 0, m_end = 0;
+  if (!grouped_tile(offsets, experts, R, mt, e, m0, m_end)) return;  // beyond the last tile: uniform
+  const int64_t wstride = (int64_t)K * (N / 2), sstride = (int64_t)(K / group) * N, zstride = (int64_t)(K / group) * (N / 2);
+  // a last column tile of at most 128 columns (N = 1408 is 5.5 tiles) runs
+  // as 256 x 128: half the MFMAs, the same dequantisation per wavefront
+  if (N - nt * BN <= BN / 2)
+    p8::tile8<2, 2>(lds, A + (int64_t)m0 * K, W + e * wstride, S + e * sstride, Z + e * zstride,
+                    Y + (int64_t)m0 * N, m_end - m0, N, K, group, Tile{0, nt * BN});
+  else
+    p8::tile8<4>(lds, A + (int64_t)m0 * K, W + e * wstride, S + e * sstride, Z + e * zstride, Y + (int64_t)m0 * N,
+                 m_end - m0, N, K, group, Tile{0, nt * BN});
 }
 
 }  // namespace w4a16
@@ -1541,12 +1554,12 @@ extern "C" tb_status tb_moe_w4a16_grouped_gemm(const uint16_t* A, const uint8_t*
   TB_CHECK_ALIGN(scales, 16, "scales");
   TB_CHECK_ALIGN(zeros, 4, "zeros");
   TB_CHECK_ALIGN(Y, 16, "Y");
-  if (tb_status st = tb::reserve_lds(reinterpret_cast<const void*>(&w4a16_grouped), LDS4_BYTES, "tb_moe_w4a16_grouped_gemm")) return st;
+  if (tb_status st = tb::reserve_lds(reinterpret_cast<const void*>(&w4a16_grouped), p8::LDS_BYTES, "tb_moe_w4a16_grouped_gemm")) return st;
   const int64_t tiles_n = (N + BN - 1) / BN;
   const int64_t tile_rows = (R + BM - 1) / BM + experts;  // upper bound on sum_e ceil(rows_e / 256)
   const int64_t blocks = tile_rows * tiles_n;
   TB_CHECK_ARG(blocks < (1ll << 31), "tb_moe_w4a16_grouped_gemm: problem too large");
-  hipLaunchKernelGGL(w4a16_grouped, dim3((unsigned)blocks), dim3(T4), LDS4_BYTES, stream,
+  hipLaunchKernelGGL(w4a16_grouped, dim3((unsigned)blocks), dim3(p8::THREADS), p8::LDS_BYTES, stream,
                      reinterpret_cast<const _Float16*>(A), W, reinterpret_cast<const _Float16*>(scales), zeros, offsets,
                      reinterpret_cast<_Float16*>(Y), (int)R, (int)experts, (int)N, (int)K, (int)group, (int)tiles_n);
   return tb::launch_status("tb_moe_w4a16_grouped_gemm");
