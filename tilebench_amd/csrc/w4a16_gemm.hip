@@ -31,43 +31,13 @@
 //           last round would be part-empty, the host may cover the last tile
 //           columns with 192-row tiles instead, so that the work splits into
 //           whole rounds more evenly.
-// The grouped GEMM (w4a16_grouped) runs the same tile on each expert's
+// The grouped GEMM (w4a16_grouped) and the MoE layer's gate/up (moe_gate_up:
+// gathered token rows, SiLU(gate) * up epilogue) and down (moe_down: routing
+// weight and scatter epilogue) projections run the same tile on each expert's
 // operands; a last column tile of at most 128 columns runs it as 256 x 128
-// (the eight wavefronts as 4 row groups x 2 column groups).
-// Every output element sees the same MFMA operands, in the same K order, as
-// in prefill_tile below, so the kernels give bit-identical results.
-//
-// MoE layer kernels (prefill_tile): one 256 x 256 output tile per
-// 512-thread block, eight wavefronts (two per SIMD) each owning a 128 x 64
-// sub-tile (8 v_mfma_f32_32x32x16_f16 accumulators = 128 fp32 per lane), K
-// advanced 64 at a time:
-//
-//   A     : streamed HBM -> LDS by the buffer unit (buffer_load ... lds, no
-//           registers), three LDS stages, issued two steps ahead;
-//   W     : packed int4 tile of step k + 1 loaded into registers during step k
-//           (each thread: 4 rows x 8 columns + its scales and zero-points),
-//           dequantised once per block ((1024 + q) via the 0x6400 magic number,
-//           exact zero-point subtraction, one RNE multiply by the scale:
-//           bit-identical to the standalone dequantiser), transposed with byte
-//           permutes so each column holds consecutive k, and written to one of
-//           two LDS stages as W^T.  The registers are consumed before the next
-//           loads are issued into them, so the wait that precedes the
-//           dequantisation only covers loads issued a full step earlier;
-//   LDS   : rows of 64 halfs in 16-byte chunks, chunk c of row r at slot
-//           c ^ ((r ^ (r >> 3)) & 7): the fragment reads (8 consecutive rows)
-//           and the W^T writes (rows 8 apart) are both free of bank conflicts;
-//   MFMA  : the fragments of k16 slice s + 1 are read while the 8 MFMAs of
-//           slice s run.  The MFMA computes the transposed product (W^T
-//           fragment as the first operand), so each lane ends with four
-//           consecutive output columns per accumulator group;
-//   order : every K step is split in two halves by a barrier.  The wavefronts
-//           of rows 0-127 run their MFMAs in the first half and dequantise in
-//           the second, those of rows 128-255 the other way round, so each
-//           SIMD always has one wavefront feeding its matrix pipe while the
-//           other keeps the vector ALU busy; the wavefront in its MFMA phase
-//           runs at raised issue priority.
-//   output: the fp16 tile is staged in LDS with 8-byte writes and stored with
-//           16-byte row stores.
+// (the eight wavefronts as 4 row groups x 2 column groups).  Every output
+// element sees the same MFMA operands in the same K order in all of them, so
+// an expert's rows equal the dense product bit for bit.
 //
 // Tiles are numbered XCD-aware: consecutive hardware block ids land on
 // different XCDs, so block ids are first regrouped so that each XCD owns a
@@ -92,87 +62,17 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int GROUP_M = 4;  // tile rows per ordering group
 
-// Code half2 pairs of one packed dword in the order columns (0,2), (4,6),
-// (1,3), (5,7): one byte permute per pair takes two code bytes from the masked
-// word and the high bytes from a constant word, so no OR is needed.  Even
-// columns (low nibbles) sit under 0x64 and read 1024 + q; odd columns keep
-// their nibble in bits 7:4 and sit under 0x54, whose mantissa unit is 1/16, so
-// they read 64 + q with no shift.  Zero-points unpacked the same way give
-// exact (1024 + q) - (1024 + z) and (64 + q) - (64 + z) = q - z.
-__device__ __forceinline__ void unpack8x(uint32_t w, f16x2 (&h)[4]) {
-  const uint32_t even = w & 0x0F0F0F0Fu;  // columns 0, 2, 4, 6
-  const uint32_t odd = w & 0xF0F0F0F0u;   // columns 1, 3, 5, 7, nibbles in bits 7:4
-  const uint32_t c64 = 0x64646464u, c54 = 0x54545454u;
-  h[0] = as_h2(perm(c64, even, 0x04010400u));
-  h[1] = as_h2(perm(c64, even, 0x04030402u));
-  h[2] = as_h2(perm(c54, odd, 0x04010400u));
-  h[3] = as_h2(perm(c54, odd, 0x04030402u));
-}
-// Scale half2 pairs (0,1), (2,3), (4,5), (6,7) reordered to unpack8x's order.
-__device__ __forceinline__ void scales_x(const u32x4 s, f16x2 (&h)[4]) {
-  h[0] = as_h2(perm(s[1], s[0], 0x05040100u));
-  h[1] = as_h2(perm(s[3], s[2], 0x05040100u));
-  h[2] = as_h2(perm(s[1], s[0], 0x07060302u));
-  h[3] = as_h2(perm(s[3], s[2], 0x07060302u));
-}
-// (1024 + q) half2 pairs of one packed dword: columns (0,1), (2,3), (4,5), (6,7).
-__device__ __forceinline__ void unpack8(uint32_t w, f16x2 (&h)[4]) {
-  const uint32_t even = w & 0x0F0F0F0Fu;
-  const uint32_t odd = (w >> 4) & 0x0F0F0F0Fu;
-  h[0] = magic_h2(perm(odd, even, 0x0C040C00u));
-  h[1] = magic_h2(perm(odd, even, 0x0C050C01u));
-  h[2] = magic_h2(perm(odd, even, 0x0C060C02u));
-  h[3] = magic_h2(perm(odd, even, 0x0C070C03u));
-}
-
 struct Tile {
   int m0, n0;
 };
 
-__device__ __forceinline__ Tile tile_of_block(int tiles_m, int tiles_n) {
-  const int nb = tiles_m * tiles_n;
-  int bid = blockIdx.x;
-  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);  // contiguous run per XCD
-  const int per_group = GROUP_M * tiles_n;
-  const int group = bid / per_group;
-  const int first_m = group * GROUP_M;
-  const int rows = min(tiles_m - first_m, GROUP_M);
-  const int in_group = bid - group * per_group;
-  Tile t;
-  t.m0 = (first_m + in_group % rows) * BM;
-  t.n0 = (in_group / rows) * BN;
-  return t;
-}
-
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 typedef int i32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 constexpr uint32_t RSRC_DW3 = 0x00020000u;
 constexpr uint32_t OOB = 0x80000000u;
-constexpr int T4 = 512;
-constexpr int A_STAGE = BM * BK;  // halfs
-constexpr int B_STAGE = BN * BK;  // halfs
-constexpr int A_STAGES = 3, B_STAGES = 2;
-constexpr size_t LDS4_BYTES = (size_t)(A_STAGES * A_STAGE + B_STAGES * B_STAGE) * 2;  // 160 KiB
-constexpr int C_STRIDE = BN + 8;  // halfs per row of the staged output tile (16 B pad)
-// the staged tile plus 256 pair ids and 256 weights fit in the stage buffers
-static_assert((size_t)BM * C_STRIDE * 2 + (size_t)BM * 8 <= (size_t)(3 * BM * BK + 2 * BN * BK) * 2, "LDS budget");
-
-__device__ __forceinline__ int swz2(int row, int chunk) { return (row * 8 + (chunk ^ ((row ^ (row >> 3)) & 7))) * 8; }
-
 __device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, (int)RSRC_DW3);
 }
-
-struct WRegs4 {
-  uint32_t w[4];
-  u32x4 s;
-  uint32_t z;
-};
-
-// How a tile finds its A rows and what its epilogue writes.
-enum ARows { A_DIRECT = 0, A_GATHER = 1 };
-enum Epilogue { EPI_PLAIN = 0, EPI_SILU_MUL = 1, EPI_SCALE_SCATTER = 2 };
 
 // Row map of the MoE pipeline's tiles: tile row m is (token, slot) pair
 // ids[m]; the pair's token is ids[m] / topk and its routing weight w[ids[m]].
@@ -189,340 +89,6 @@ struct RowMap {
 __device__ __forceinline__ _Float16 h_of_rounded(float f) {
   asm volatile("" : "+v"(f));
   return (_Float16)f;
-}
-
-// One 256 x 256 tile: rows [m0, m_end) of A (A holds a_rows rows in all),
-// columns [n0, n0 + 256) of W (N columns), full K.  Shared by the dense kernel
-// and the grouped (MoE) kernels, which pass one expert's W / scales / zeros.
-//   A_GATHER          : tile row m reads A row rm.ids[m] / rm.topk (a token of
-//                       the activations) instead of row m;
-//   EPI_SILU_MUL      : the tile's W columns are gate columns [n0/2, n0/2 + 128)
-//                       and up columns N/2 + [n0/2, n0/2 + 128) of W13 (N = 2I);
-//                       Y (row stride N/2) gets fp16(silu(g) * u) of the fp16
-//                       gate and up values, columns n0/2 ..;
-//   EPI_SCALE_SCATTER : the fp32 accumulator of row m is multiplied by
-//                       rm.w[rm.ids[m]] before rounding, and the row is stored
-//                       at row rm.ids[m] of Y through the staged tile (whole
-//                       512-byte row segments; 8-byte stores straight from the
-//                       accumulators measured 13 % slower).
-template <int AR, int EPI, bool NW = false>
-__device__ __forceinline__ void prefill_tile(_Float16* __restrict__ lds, const _Float16* __restrict__ A,
-                                             const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
-                                             const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int a_rows,
-                                             int m0, int m_end, int n0, int N, int K, int group,
-                                             const RowMap rm = RowMap{}) {
-  // NW (narrow): the tile's columns are n0 .. n0 + 127 (a last tile of at most
-  // 128 columns; with EPI_SILU_MUL, 64 gate and 64 up columns); each wavefront
-  // owns 32 of them (one B fragment instead of two) and each thread
-  // dequantises 2 rows x 8 columns instead of 4 x 8.
-  constexpr int NJ = NW ? 1 : 2;    // 32-column B fragments per wavefront
-  constexpr int RPT = NW ? 2 : 4;   // W rows per dequantising thread
-  constexpr int HG = NW ? 8 : 16;   // EPI_SILU_MUL: column groups of 8 per gate / up half
-  _Float16* const lds_a = lds;
-  _Float16* const lds_b = lds + A_STAGES * A_STAGE;
-  const Tile tile{m0, n0};
-  const int M = m_end;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 2, wn = wave & 3;
-
-  const rsrc_t rw = make_rsrc(W, (uint32_t)K * (uint32_t)(N / 2));
-  const rsrc_t rs = make_rsrc(S, (uint32_t)(K / group) * (uint32_t)N * 2u);
-  const rsrc_t rz = make_rsrc(Z, (uint32_t)(K / group) * (uint32_t)(N / 2));
-  i32x4 ra4;
-  {
-    const uint64_t base = (uint64_t)(uintptr_t)A;
-    ra4[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)base);
-    ra4[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(base >> 32) & 0xFFFF);
-    ra4[2] = __builtin_amdgcn_readfirstlane((int)((uint32_t)a_rows * (uint32_t)K * 2u));
-    ra4[3] = (int)RSRC_DW3;
-  }
-
-  // Scatter epilogue: thread t < 256 fetches row t's pair id now and its
-  // routing weight after the prologue's first wait, so neither load's latency
-  // lands in the epilogue.
-  int pf_pid = -1;
-  float pf_w = 0.f;
-  if (EPI == EPI_SCALE_SCATTER && t < BM) {
-    const int m = tile.m0 + t;
-    pf_pid = m < M ? rm.ids[m] : -1;
-  }
-
-  // A DMA: 32 instructions of 1 KiB (8 rows) per tile, 4 per wavefront.
-  uint32_t a_off[4];
-  {
-    const int lr = lane >> 3;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = (wave * 4 + i) * 8 + lr;
-      const int lc = (lane & 7) ^ ((row ^ (row >> 3)) & 7);
-      const int m = tile.m0 + row;
-      int src = m;
-      if (AR == A_GATHER && m < M) {
-        const int pid = rm.ids[m];
-        src = (unsigned)pid < (unsigned)rm.pairs ? pid / rm.topk : a_rows;  // a bad id reads zeros
-      }
-      a_off[i] = m < M && src < a_rows ? ((uint32_t)src * (uint32_t)K + (uint32_t)lc * 8u) * 2u : OOB;
-    }
-  }
-  const uint32_t a_lds0 = (uint32_t)__builtin_amdgcn_readfirstlane(
-      (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_a) + (uint32_t)(wave * 4 * 1024);
-
-  // W: thread owns rows kq*RPT .. kq*RPT+RPT-1 of the 64-row step, columns cg*8 .. +7.
-  const int cg = NW ? (t & 15) : (t & 31), kq = NW ? (t >> 4) : (t >> 5);
-  int n = tile.n0 + cg * 8;
-  bool n_ok = n < N;
-  if (EPI == EPI_SILU_MUL) {
-    const int half_cols = N / 2, a0 = tile.n0 / 2 + (cg & (HG - 1)) * 8;  // activation column of this group
-    n = (cg < HG ? 0 : half_cols) + a0;
-    n_ok = a0 < half_cols;
-  }
-  const uint32_t w_row = (uint32_t)(N / 2);
-  const uint32_t w_off = n_ok ? (uint32_t)(kq * RPT) * w_row + (uint32_t)(n / 2) : OOB;
-  const uint32_t s_off = n_ok ? (uint32_t)n * 2u : OOB;
-  const uint32_t z_off = n_ok ? (uint32_t)(n / 2) : OOB;
-  // W^T write addresses in bytes from the LDS base (stage 0); stage 1 adds a
-  // constant that fits the LDS instructions' offset field, so a write takes no
-  // address arithmetic once the stage is a compile-time constant.
-  uint32_t b_st[8];
-#pragma unroll
-  for (int c = 0; c < 8; ++c)
-    b_st[c] = (uint32_t)(A_STAGES * A_STAGE +
-                         (NW ? swz2(cg * 8 + c, kq >> 2) + (kq & 3) * 2 : swz2(cg * 8 + c, kq >> 1) + (kq & 1) * 4)) * 2u;
-
-  // fragment read offsets (halfs) for k16 step ks and row parity of the fragment index
-  const int fa_base = (wm * 128 + (lane & 31)) * 64;
-  const int fb_base = (wn * 32 * NJ + (lane & 31)) * 64;
-  int fx[4][2];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-    for (int ip = 0; ip < 2; ++ip) {
-      const int r = ip * 32 + (lane & 31);
-      fx[ks][ip] = ((ks * 2 + (lane >> 5)) ^ ((r ^ (r >> 3)) & 7)) * 8;
-    }
-
-  auto issue_a = [&](int kt) {
-    const uint32_t st = a_lds0 + (uint32_t)((kt % A_STAGES) * A_STAGE * 2);
-    const uint32_t soff = (uint32_t)(kt * BK) * 2u;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                   :
-                   : "s"(__builtin_amdgcn_readfirstlane((int)(st + (uint32_t)(i * 1024)))), "v"(a_off[i]), "s"(ra4),
-                     "s"(__builtin_amdgcn_readfirstlane((int)soff))
-                   : "memory", "m0");
-    }
-  };
-  auto issue_w = [&](WRegs4& r, int kt) {
-    const uint32_t k0 = (uint32_t)(kt * BK);
-    const uint32_t kw = k0 * w_row;
-#pragma unroll
-    for (int q = 0; q < RPT; ++q) r.w[q] = __builtin_amdgcn_raw_buffer_load_b32(rw, w_off + q * w_row, kw, 0);
-    const uint32_t g = k0 / (uint32_t)group;
-    r.s = __builtin_amdgcn_raw_buffer_load_b128(rs, s_off, g * (uint32_t)N * 2u, 0);
-    r.z = __builtin_amdgcn_raw_buffer_load_b32(rz, z_off, g * w_row, 0);
-  };
-  auto dequant_store = [&](const WRegs4& r, auto stage) {
-    char* const st = reinterpret_cast<char*>(lds) + decltype(stage)::value * B_STAGE * 2;
-    f16x2 zh[4], sh[4];
-    unpack8x(r.z, zh);
-    scales_x(r.s, sh);
-    uint32_t d[4][4];
-#pragma unroll
-    for (int q = 0; q < RPT; ++q) {
-      f16x2 h[4];
-      unpack8x(r.w[q], h);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) d[q][j] = as_u32((h[j] - zh[j]) * sh[j]);
-    }
-    // column cc of the 8 is pair (cc & 1) * 2 + (cc >> 2), half (cc >> 1) & 1
-#pragma unroll
-    for (int cc = 0; cc < 8; ++cc) {
-      const int pj = (cc & 1) * 2 + (cc >> 2);
-      const uint32_t sel = ((cc >> 1) & 1) ? 0x07060302u : 0x05040100u;
-      if constexpr (NW) {
-        *reinterpret_cast<uint32_t*>(st + b_st[cc]) = perm(d[1][pj], d[0][pj], sel);
-      } else {
-        u32x2v col;
-        col[0] = perm(d[1][pj], d[0][pj], sel);
-        col[1] = perm(d[3][pj], d[2][pj], sel);
-        *reinterpret_cast<u32x2v*>(st + b_st[cc]) = col;
-      }
-    }
-  };
-
-  f32x16 acc[4][2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-
-  // The MFMA computes the transposed product (W^T fragment as the A operand,
-  // A fragment as the B operand): lane l then holds output row l % 32 and four
-  // consecutive output columns per group of four accumulator elements.
-  auto read_frags = [&](const _Float16* sa, const _Float16* sb, int ks, h8 (&fa)[4], h8 (&fb)[2]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) fa[i] = *reinterpret_cast<const h8*>(sa + fa_base + i * 32 * 64 + fx[ks][i & 1]);
-    // The swizzle of LDS row R depends on bit 5 of R: R = wn * 64 + j * 32 + lane % 32
-    // has it from j, a narrow tile's R = wn * 32 + lane % 32 from wn.
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-      fb[j] = *reinterpret_cast<const h8*>(sb + fb_base + j * 32 * 64 + fx[ks][NW ? (wn & 1) : (j & 1)]);
-  };
-  auto mfma_stage = [&](const _Float16* sa, const _Float16* sb) {
-    h8 fa[2][4], fb[2][2];
-    read_frags(sa, sb, 0, fa[0], fb[0]);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int cur = ks & 1;
-      // reads of slice ks + 1 go out before the MFMAs of slice ks, so their
-      // latency hides behind eight MFMAs
-      if (ks < 3) read_frags(sa, sb, ks + 1, fa[cur ^ 1], fb[cur ^ 1]);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[cur][j], fa[cur][i], acc[i][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-
-  constexpr int WAIT_VM0 = 0 | (7 << 4) | (15 << 8);
-  const int nk = K / BK;
-  WRegs4 wr;
-  issue_a(0);
-  if (nk > 1) issue_a(1);
-  issue_w(wr, 0);
-  __builtin_amdgcn_s_waitcnt(WAIT_VM0);
-  if (EPI == EPI_SCALE_SCATTER && (unsigned)pf_pid < (unsigned)rm.pairs) pf_w = rm.w[pf_pid];
-  dequant_store(wr, std::integral_constant<int, 0>{});
-  if (nk > 1) issue_w(wr, 1);
-  __syncthreads();
-
-  // Step kt: MFMAs on A(kt), W(kt); dequantise W(kt + 1) (loaded one step
-  // earlier); then issue A(kt + 2) and W(kt + 2).  Consuming the registers
-  // before re-issuing into them keeps one W register set, and the wait before
-  // the dequantisation only covers loads issued a full step earlier.
-  // The W^T stage alternates with kt; the loop below is unrolled by two so that
-  // it is a constant (SB = kt & 1) in each copy.
-  auto dequant_and_issue = [&](int kt, auto next_stage) {
-    if (kt + 1 < nk) {
-      __builtin_amdgcn_s_waitcnt(WAIT_VM0);
-      dequant_store(wr, next_stage);
-    }
-    if (kt + 2 < nk) {
-      issue_a(kt + 2);
-      issue_w(wr, kt + 2);
-    }
-  };
-  auto step = [&](int kt, auto sbc) {
-    constexpr int SB = decltype(sbc)::value;
-    const std::integral_constant<int, SB ^ 1> next{};
-    if (wm == 1) {
-      dequant_and_issue(kt, next);
-      __builtin_amdgcn_s_barrier();
-      __builtin_amdgcn_s_setprio(1);
-      mfma_stage(lds_a + (kt % A_STAGES) * A_STAGE, lds_b + SB * B_STAGE);
-      __builtin_amdgcn_s_setprio(0);
-    } else {
-      __builtin_amdgcn_s_setprio(1);
-      mfma_stage(lds_a + (kt % A_STAGES) * A_STAGE, lds_b + SB * B_STAGE);
-      __builtin_amdgcn_s_setprio(0);
-      __builtin_amdgcn_s_barrier();
-      dequant_and_issue(kt, next);
-    }
-    __syncthreads();
-  };
-  int kt = 0;
-  for (; kt + 1 < nk; kt += 2) {
-    step(kt, std::integral_constant<int, 0>{});
-    step(kt + 1, std::integral_constant<int, 1>{});
-  }
-  if (kt < nk) step(kt, std::integral_constant<int, 0>{});
-
-  // Epilogue: stage the fp16 tile in LDS, then store 16-byte row chunks.
-  // Accumulator elements 4g .. 4g+3 of fragment (i, j) are row i*32 + lane%32,
-  // columns j*32 + g*8 + (lane/32)*4 + 0..3 of the wave tile.
-  _Float16* ct = lds;
-  // per-row pair ids and weights of the scatter epilogue, past the staged tile
-  int* const row_pid = reinterpret_cast<int*>(lds + BM * C_STRIDE);
-  float* const row_wl = reinterpret_cast<float*>(row_pid + BM);
-  float row_w[4] = {1.f, 1.f, 1.f, 1.f};
-  if (EPI == EPI_SCALE_SCATTER) {
-    if (t < BM) {
-      row_pid[t] = pf_pid;
-      row_wl[t] = pf_w;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) row_w[i] = row_wl[wm * 128 + i * 32 + (lane & 31)];
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int row = wm * 128 + i * 32 + (lane & 31);
-        const int col = wn * 32 * NJ + j * 32 + g * 8 + (lane >> 5) * 4;
-        _Float16 h[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          h[e] = EPI == EPI_SCALE_SCATTER ? h_of_rounded(acc[i][j][4 * g + e] * row_w[i]) : (_Float16)acc[i][j][4 * g + e];
-        u32x2v v;
-        v[0] = as_u32(f16x2{h[0], h[1]});
-        v[1] = as_u32(f16x2{h[2], h[3]});
-        *reinterpret_cast<u32x2v*>(ct + row * C_STRIDE + col) = v;
-      }
-  __syncthreads();
-  const int rows = min(BM, M - tile.m0);
-  if (EPI == EPI_SILU_MUL) {
-    // 128 activation columns per tile (64 when narrow): gate in staged columns
-    // 0 .. 8 HG - 1, up in 8 HG .. 16 HG - 1
-    const int half_cols = N / 2, a0 = tile.n0 / 2;
-    const int acols = min(8 * HG, half_cols - a0);
-#pragma unroll 4
-    for (int idx = t; idx < BM * (BN / 16); idx += T4) {
-      const int row = idx >> 4, ch = idx & 15;
-      if (row < rows && ch * 8 < acols) {
-        const u32x4 gv = *reinterpret_cast<const u32x4*>(ct + row * C_STRIDE + ch * 8);
-        const u32x4 uv = *reinterpret_cast<const u32x4*>(ct + row * C_STRIDE + 8 * HG + ch * 8);
-        u32x4 o;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const f16x2 g2 = as_h2(gv[q]), u2 = as_h2(uv[q]);
-          _Float16 r[2];
-#pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            const float g = (float)g2[e], u = (float)u2[e];
-            float sg = 1.0f + expf(-g);
-            asm volatile("" : "+v"(sg));
-            const float si = g / sg;
-            r[e] = h_of_rounded(si * u);
-          }
-          o[q] = as_u32(f16x2{r[0], r[1]});
-        }
-        *reinterpret_cast<u32x4*>(Y + (int64_t)(tile.m0 + row) * half_cols + a0 + ch * 8) = o;
-      }
-    }
-    return;
-  }
-  const int cols = min(BN, N - tile.n0);
-#pragma unroll 4
-  for (int idx = t; idx < BM * (BN / 8); idx += T4) {
-    const int row = idx >> 5, ch = idx & 31;
-    if (row < rows && ch * 8 < cols) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(ct + row * C_STRIDE + ch * 8);
-      int64_t dst = tile.m0 + row;
-      if (EPI == EPI_SCALE_SCATTER) {
-        const int pid = row_pid[row];
-        if ((unsigned)pid >= (unsigned)rm.pairs) continue;
-        dst = pid;
-      }
-      *reinterpret_cast<u32x4*>(Y + dst * N + tile.n0 + ch * 8) = v;
-    }
-  }
 }
 
 // Expert and row range of grouped tile row mt: rows offsets[e] .. offsets[e+1]
@@ -572,57 +138,6 @@ __device__ __forceinline__ int grouped_block_id() {
   int bid = blockIdx.x;
   if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
   return bid;
-}
-
-// MoE gate/up projection: rows of the pair space (sorted by expert, offsets[e]
-// .. offsets[e+1] for expert e) gather their token's activation row X[ids[m] /
-// topk], multiply by expert e's W13 [K, 2I] and write fp16(silu(gate) * up),
-// I columns per row, in the same sorted row order.  128 output columns per tile.
-__global__ void __launch_bounds__(T4, 1)
-    moe_gate_up(const _Float16* __restrict__ X, const int* __restrict__ ids, const int* __restrict__ offsets,
-                const uint8_t* __restrict__ W, const _Float16* __restrict__ S, const uint8_t* __restrict__ Z,
-                _Float16* __restrict__ act, int tokens, int topk, int pairs, int experts, int I, int K, int group,
-                int tiles_n) {
-  extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
-  const int bid = grouped_block_id();
-  const int mt = bid / tiles_n, nt = bid - mt * tiles_n;
-  int e = 0, m0 = 0, m_end = 0;
-  if (!grouped_tile(offsets, experts, pairs, mt, e, m0, m_end)) return;
-  const int N = 2 * I;
-  const int64_t wstride = (int64_t)K * I, sstride = (int64_t)(K / group) * N, zstride = (int64_t)(K / group) * I;
-  RowMap rm;
-  rm.ids = ids;
-  rm.topk = topk;
-  rm.pairs = pairs;
-  // a last tile of at most 64 activation columns (I = 704 is 5.5 tiles) takes the narrow form
-  if (I - nt * (BN / 2) <= BN / 4)
-    prefill_tile<A_GATHER, EPI_SILU_MUL, true>(lds, X, W + e * wstride, S + e * sstride, Z + e * zstride, act, tokens,
-                                               m0, m_end, nt * BN, N, K, group, rm);
-  else
-    prefill_tile<A_GATHER, EPI_SILU_MUL>(lds, X, W + e * wstride, S + e * sstride, Z + e * zstride, act, tokens, m0,
-                                         m_end, nt * BN, N, K, group, rm);
-}
-
-// MoE down projection: sorted activation rows times expert e's W2 [I, H]; row m
-// is scaled by its pair's routing weight w[ids[m]] in fp32 and stored, as fp16,
-// at row ids[m] of Y [pairs, H] (token-major: pair t * topk + j).
-__global__ void __launch_bounds__(T4, 1)
-    moe_down(const _Float16* __restrict__ act, const int* __restrict__ ids, const int* __restrict__ offsets,
-             const float* __restrict__ w, const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
-             const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int pairs, int experts, int H, int I,
-             int group, int tiles_n) {
-  extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
-  const int bid = grouped_block_id();
-  const int mt = bid / tiles_n, nt = bid - mt * tiles_n;
-  int e = 0, m0 = 0, m_end = 0;
-  if (!grouped_tile(offsets, experts, pairs, mt, e, m0, m_end)) return;
-  const int64_t wstride = (int64_t)I * (H / 2), sstride = (int64_t)(I / group) * H, zstride = (int64_t)(I / group) * (H / 2);
-  RowMap rm;
-  rm.ids = ids;
-  rm.w = w;
-  rm.pairs = pairs;
-  prefill_tile<A_DIRECT, EPI_SCALE_SCATTER>(lds, act, W + e * wstride, S + e * sstride, Z + e * zstride, Y, pairs,
-                                            m0, m_end, nt * BN, H, I, group, rm);
 }
 
 // ---------------------------------------------------------------------------
@@ -986,16 +501,36 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t c
   return r;
 }
 
+// What a tile reads and writes besides the plain product.
+enum TileMode {
+  T_PLAIN = 0,    // rows m < M of A and Y
+  T_GATE_UP = 1,  // MoE gate/up: see below
+  T_DOWN = 2      // MoE down: see below
+};
+
 // One tile at (m0, n0): the eight wavefronts as 8 / WN row groups of 32 MB
 // rows times WN column groups of 64 columns.  WN = 4: 256 columns and 64 MB
 // rows (MB = 4: 256, MB = 3: 192); WN = 2, MB = 2: 256 rows x 128 columns,
-// for a last column tile of at most 128 columns.
-template <int MB, int WN = 4>
+// for a last column tile of at most 128 columns.  Rows m < M exist; A holds
+// a_rows rows.
+//   T_GATE_UP: tile row m reads A row rm.ids[m] / rm.topk (a token; a bad id
+//     reads zeros).  W is W13 [K, N = 2I]; the tile covers activation columns
+//     a0 = n0 / 2 .. a0 + 127, and column group wn takes gate columns
+//     a0 + 32 wn .. + 31 as its first 16 packed bytes and the up columns of the
+//     same activation columns (I + ...) as its last 16, so a lane ends with
+//     the gate and the up sum of the same activation columns (accumulator
+//     elements 4g + e and 4(g + 2) + e).  Y [M, I] gets fp16(silu(g) * u) of
+//     the fp16-rounded gate and up values.
+//   T_DOWN: row m's fp32 sums are multiplied by rm.w[rm.ids[m]], rounded once
+//     to fp16 and stored at row rm.ids[m] of Y (rows with a bad id are not
+//     stored).
+template <int MB, int WN = 4, int MODE = T_PLAIN>
 __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16* __restrict__ A,
                                       const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
                                       const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int M, int N, int K,
-                                      int group, const Tile tile) {
+                                      int group, const Tile tile, int a_rows = -1, const RowMap rm = RowMap{}) {
   static_assert((WN == 4 && (MB == 3 || MB == 4)) || (WN == 2 && MB == 2), "tile8 shapes");
+  if (MODE == T_PLAIN) a_rows = M;
   constexpr int TM = 32 * MB * (8 / WN);  // tile rows
   constexpr int AI = TM / 64;             // A DMA instructions per wavefront and step (8 rows each)
   constexpr int DMA_PER_STEP = AI + 5;
@@ -1005,7 +540,8 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
   const int nk = K / BK;
   const uint32_t half_n = (uint32_t)(N / 2);
 
-  const i32x4 ra = rsrc4(A, (uint32_t)M * (uint32_t)K * 2u);
+  const i32x4 ra = rsrc4(A, (uint32_t)a_rows * (uint32_t)K * 2u);
+  const int I = N / 2, a0 = tile.n0 / 2;  // T_GATE_UP: activation columns
   const i32x4 rw = rsrc4(W, (uint32_t)K * half_n);
   const i32x4 rs = rsrc4(S, (uint32_t)(K / group) * (uint32_t)N * 2u);
   const i32x4 rz = rsrc4(Z, (uint32_t)(K / group) * half_n);
@@ -1018,7 +554,12 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
     const int row = 8 * (AI * w + i) + (lane >> 3);
     const int c = (lane & 7) ^ ((row ^ (row >> 3)) & 7);
     const int m = tile.m0 + row;
-    a_off[i] = m < M ? ((uint32_t)m * (uint32_t)K + (uint32_t)c * 8u) * 2u : OOB;
+    int src = m;
+    if (MODE == T_GATE_UP && m < M) {
+      const int pid = rm.ids[m];
+      src = (unsigned)pid < (unsigned)rm.pairs ? pid / rm.topk : a_rows;
+    }
+    a_off[i] = m < M && src < a_rows ? ((uint32_t)src * (uint32_t)K + (uint32_t)c * 8u) * 2u : OOB;
   }
   // W DMA: instruction i of wavefront w fills rows 8w + 2i, +1 (lane L: row +
   // L / 32, dword L % 32 of the row, i.e. 16-byte slot (L % 32) / 4, which
@@ -1028,8 +569,16 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
   for (int i = 0; i < 4; ++i) {
     const int r = 8 * w + 2 * i + (lane >> 5);
     const int c = ((lane & 31) >> 2) ^ (r & 7);
-    const uint32_t col = (uint32_t)(tile.n0 / 2 + c * 16 + (lane & 3) * 4);
-    w_off[i] = col < half_n ? (uint32_t)r * half_n + col : OOB;
+    if (MODE == T_GATE_UP) {
+      // chunk c: gate (c even) or up (c odd) of activation columns a0 + 32 (c / 2) ..,
+      // this dword their 8 columns from a0 + 32 (c / 2) + 8 (lane % 4)
+      const int acol = a0 + 32 * (c >> 1) + 8 * (lane & 3);
+      const uint32_t byte = (uint32_t)((c & 1) * (I / 2) + acol / 2);
+      w_off[i] = acol < I ? (uint32_t)r * half_n + byte : OOB;
+    } else {
+      const uint32_t col = (uint32_t)(tile.n0 / 2 + c * 16 + (lane & 3) * 4);
+      w_off[i] = col < half_n ? (uint32_t)r * half_n + col : OOB;
+    }
   }
   // Scales and zero-points of a step's group: wavefronts 0 and 1 fetch the
   // 512 scale bytes, wavefront 2 the 128 zero-point bytes (lanes 32..63 land
@@ -1037,12 +586,26 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
   uint32_t sz_off = OOB, sz_lds = PAD_OFF;
   const i32x4& rsz = w == 2 ? rz : rs;
   if (w < 2) {
-    const uint32_t col = (uint32_t)tile.n0 + (uint32_t)(w * 128 + lane * 2);
-    sz_off = col < (uint32_t)N ? col * 2u : OOB;
+    if (MODE == T_GATE_UP) {
+      // scale slot t = 128 w + 2 lane (two columns) of column group t / 64:
+      // gate (t % 64 < 32) or up of activation column a0 + 32 (t / 64) + t % 32
+      const int t2 = 128 * w + 2 * lane, acol = a0 + 32 * (t2 >> 6) + (t2 & 31);
+      sz_off = acol < I ? (uint32_t)(((t2 & 32) ? I : 0) + acol) * 2u : OOB;
+    } else {
+      const uint32_t col = (uint32_t)tile.n0 + (uint32_t)(w * 128 + lane * 2);
+      sz_off = col < (uint32_t)N ? col * 2u : OOB;
+    }
     sz_lds = S_OFF + w * 256;
   } else if (w == 2) {
-    const uint32_t col = (uint32_t)(tile.n0 / 2 + lane * 4);
-    sz_off = lane < 32 && col < half_n ? col : OOB;
+    if (MODE == T_GATE_UP) {
+      // zero-point bytes b = 4 lane .. + 3 of column group b / 32: gate
+      // (b % 32 < 16) or up bytes of activation columns a0 + 32 (b / 32) + 2 (b % 16) ..
+      const int b = 4 * lane, acol = a0 + 32 * (b >> 5) + 2 * (b & 15);
+      sz_off = lane < 32 && acol < I ? (uint32_t)(((b & 16) ? I / 2 : 0) + acol / 2) : OOB;
+    } else {
+      const uint32_t col = (uint32_t)(tile.n0 / 2 + lane * 4);
+      sz_off = lane < 32 && col < half_n ? col : OOB;
+    }
     sz_lds = Z_OFF;
   }
   const uint32_t lds0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)(
@@ -1105,6 +668,18 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
   }
 
   f32x16 acc[MB][2];
+
+  // T_DOWN: the pair id of each of the lane's rows now, its routing weight
+  // after the prologue, so that neither load's latency lands in the epilogue
+  int row_pid[MODE == T_DOWN ? MB : 1];
+  float row_w[MODE == T_DOWN ? MB : 1];
+  if (MODE == T_DOWN) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int m = tile.m0 + 32 * (MB * wm + mb) + j;
+      row_pid[mb] = m < M ? rm.ids[m] : -1;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < MB; ++i) acc[i][0] = acc[i][1] = f32x16{};
 
@@ -1166,6 +741,11 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
   __builtin_amdgcn_s_waitcnt(WAIT_PRO);
   barrier();
   load_scales(0);
+  if (MODE == T_DOWN) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+      row_w[mb] = (unsigned)row_pid[mb] < (unsigned)rm.pairs ? rm.w[row_pid[mb]] : 0.f;
+  }
   v2i xs[4];
   {
 #pragma unroll
@@ -1244,18 +824,57 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
 
   // Epilogue: element 4g + e of accumulator (mb, nb) is row 32 (MB wm + mb) + j,
   // column 64 wn + 16 g + 8 h + 2 e + nb of the tile.
+  if (MODE == T_GATE_UP) {
+    // g = 0, 1: gate of activation columns a0 + 32 wn + 16 g + 8 h + 2 e + nb;
+    // g + 2: up of the same columns
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int m = tile.m0 + 32 * (MB * wm + mb) + j;
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const int acol = a0 + 32 * wn + 16 * g + 8 * h;
+        u32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          _Float16 r[2];
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb) {
+            const float gv = (float)(_Float16)acc[mb][nb][4 * g + e];
+            const float uv = (float)(_Float16)acc[mb][nb][4 * (g + 2) + e];
+            float sg = 1.0f + expf(-gv);
+            asm volatile("" : "+v"(sg));
+            r[nb] = h_of_rounded(gv / sg * uv);
+          }
+          v[e] = as_u32(f16x2{r[0], r[1]});
+        }
+        if (m < M && acol < I) *reinterpret_cast<u32x4*>(Y + (int64_t)m * I + acol) = v;
+      }
+    }
+    return;
+  }
   const int col0 = tile.n0 + 64 * wn + 8 * h;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int m = tile.m0 + 32 * (MB * wm + mb) + j;
+    int64_t dst = m;
+    float rw = 1.f;
+    if (MODE == T_DOWN) {
+      dst = row_pid[mb];
+      rw = row_w[mb];
+    }
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int n = col0 + 16 * g;
       u32x4 v;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        v[e] = as_u32(f16x2{(_Float16)acc[mb][0][4 * g + e], (_Float16)acc[mb][1][4 * g + e]});
-      if (m < M && n < N) *reinterpret_cast<u32x4*>(Y + (int64_t)m * N + n) = v;
+      for (int e = 0; e < 4; ++e) {
+        if (MODE == T_DOWN)
+          v[e] = as_u32(f16x2{h_of_rounded(acc[mb][0][4 * g + e] * rw), h_of_rounded(acc[mb][1][4 * g + e] * rw)});
+        else
+          v[e] = as_u32(f16x2{(_Float16)acc[mb][0][4 * g + e], (_Float16)acc[mb][1][4 * g + e]});
+      }
+      const bool ok = MODE == T_DOWN ? (unsigned)dst < (unsigned)rm.pairs : m < M;
+      if (ok && n < N) *reinterpret_cast<u32x4*>(Y + dst * N + n) = v;
     }
   }
 }
@@ -1310,6 +929,63 @@ __global__ void __launch_bounds__(p8::THREADS, 1)
   else
     p8::tile8<4>(lds, A + (int64_t)m0 * K, W + e * wstride, S + e * sstride, Z + e * zstride, Y + (int64_t)m0 * N,
                  m_end - m0, N, K, group, Tile{0, nt * BN});
+}
+
+// MoE gate/up projection: rows of the pair space (sorted by expert, offsets[e]
+// .. offsets[e+1] for expert e) gather their token's activation row X[ids[m] /
+// topk], multiply by expert e's W13 [K, 2I] and write fp16(silu(gate) * up),
+// I columns per row, in the same sorted row order.  128 activation columns per
+// tile (64 for a last tile of at most 64: the 256 x 128 layout).
+__global__ void __launch_bounds__(p8::THREADS, 1)
+    moe_gate_up(const _Float16* __restrict__ X, const int* __restrict__ ids, const int* __restrict__ offsets,
+                const uint8_t* __restrict__ W, const _Float16* __restrict__ S, const uint8_t* __restrict__ Z,
+                _Float16* __restrict__ act, int tokens, int topk, int pairs, int experts, int I, int K, int group,
+                int tiles_n) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 lds_h[];
+  uint8_t* const lds = reinterpret_cast<uint8_t*>(lds_h);
+  const int bid = grouped_block_id();
+  const int mt = bid / tiles_n, nt = bid - mt * tiles_n;
+  int e = 0, m0 = 0, m_end = 0;
+  if (!grouped_tile(offsets, experts, pairs, mt, e, m0, m_end)) return;
+  const int N = 2 * I;
+  const int64_t wstride = (int64_t)K * I, sstride = (int64_t)(K / group) * N, zstride = (int64_t)(K / group) * I;
+  RowMap rm;
+  rm.ids = ids + m0;
+  rm.topk = topk;
+  rm.pairs = pairs;
+  if (I - nt * (BN / 2) <= BN / 4)
+    p8::tile8<2, 2, p8::T_GATE_UP>(lds, X, W + e * wstride, S + e * sstride, Z + e * zstride, act + (int64_t)m0 * I,
+                                   m_end - m0, N, K, group, Tile{0, nt * BN}, tokens, rm);
+  else
+    p8::tile8<4, 4, p8::T_GATE_UP>(lds, X, W + e * wstride, S + e * sstride, Z + e * zstride, act + (int64_t)m0 * I,
+                                   m_end - m0, N, K, group, Tile{0, nt * BN}, tokens, rm);
+}
+
+// MoE down projection: sorted activation rows times expert e's W2 [I, H]; row m
+// is scaled by its pair's routing weight w[ids[m]] in fp32 and stored, as fp16,
+// at row ids[m] of Y [pairs, H] (token-major: pair t * topk + j).
+__global__ void __launch_bounds__(p8::THREADS, 1)
+    moe_down(const _Float16* __restrict__ act, const int* __restrict__ ids, const int* __restrict__ offsets,
+             const float* __restrict__ w, const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
+             const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int pairs, int experts, int H, int I,
+             int group, int tiles_n) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 lds_h[];
+  uint8_t* const lds = reinterpret_cast<uint8_t*>(lds_h);
+  const int bid = grouped_block_id();
+  const int mt = bid / tiles_n, nt = bid - mt * tiles_n;
+  int e = 0, m0 = 0, m_end = 0;
+  if (!grouped_tile(offsets, experts, pairs, mt, e, m0, m_end)) return;
+  const int64_t wstride = (int64_t)I * (H / 2), sstride = (int64_t)(I / group) * H, zstride = (int64_t)(I / group) * (H / 2);
+  RowMap rm;
+  rm.ids = ids + m0;
+  rm.w = w;
+  rm.pairs = pairs;
+  if (H - nt * BN <= BN / 2)
+    p8::tile8<2, 2, p8::T_DOWN>(lds, act + (int64_t)m0 * I, W + e * wstride, S + e * sstride, Z + e * zstride, Y,
+                                m_end - m0, H, I, group, Tile{0, nt * BN}, m_end - m0, rm);
+  else
+    p8::tile8<4, 4, p8::T_DOWN>(lds, act + (int64_t)m0 * I, W + e * wstride, S + e * sstride, Z + e * zstride, Y,
+                                m_end - m0, H, I, group, Tile{0, nt * BN}, m_end - m0, rm);
 }
 
 }  // namespace w4a16
@@ -1588,12 +1264,12 @@ extern "C" tb_status tb_moe_w4a16_gate_up(const uint16_t* X, const int32_t* sort
   TB_CHECK_ALIGN(S13, 16, "S13");
   TB_CHECK_ALIGN(Z13, 4, "Z13");
   TB_CHECK_ALIGN(act, 16, "act");
-  if (tb_status st = tb::reserve_lds(reinterpret_cast<const void*>(&moe_gate_up), LDS4_BYTES, fn)) return st;
+  if (tb_status st = tb::reserve_lds(reinterpret_cast<const void*>(&moe_gate_up), p8::LDS_BYTES, fn)) return st;
   const int64_t tiles_n = (I + BN / 2 - 1) / (BN / 2);
   const int64_t tile_rows = (pairs + BM - 1) / BM + experts;
   const int64_t blocks = tile_rows * tiles_n;
   TB_CHECK_ARG(blocks < (1ll << 31), "%s: problem too large", fn);
-  hipLaunchKernelGGL(moe_gate_up, dim3((unsigned)blocks), dim3(T4), LDS4_BYTES, stream,
+  hipLaunchKernelGGL(moe_gate_up, dim3((unsigned)blocks), dim3(p8::THREADS), p8::LDS_BYTES, stream,
                      reinterpret_cast<const _Float16*>(X), sorted_ids, offsets, W13,
                      reinterpret_cast<const _Float16*>(S13), Z13, reinterpret_cast<_Float16*>(act), (int)tokens,
                      (int)topk, (int)pairs, (int)experts, (int)I, (int)H, (int)group, (int)tiles_n);
@@ -1620,12 +1296,12 @@ extern "C" tb_status tb_moe_w4a16_down(const uint16_t* act, const int32_t* sorte
   TB_CHECK_ALIGN(S2, 16, "S2");
   TB_CHECK_ALIGN(Z2, 4, "Z2");
   TB_CHECK_ALIGN(Y, 16, "Y");
-  if (tb_status st = tb::reserve_lds(reinterpret_cast<const void*>(&moe_down), LDS4_BYTES, fn)) return st;
+  if (tb_status st = tb::reserve_lds(reinterpret_cast<const void*>(&moe_down), p8::LDS_BYTES, fn)) return st;
   const int64_t tiles_n = (H + BN - 1) / BN;
   const int64_t tile_rows = (pairs + BM - 1) / BM + experts;
   const int64_t blocks = tile_rows * tiles_n;
   TB_CHECK_ARG(blocks < (1ll << 31), "%s: problem too large", fn);
-  hipLaunchKernelGGL(moe_down, dim3((unsigned)blocks), dim3(T4), LDS4_BYTES, stream,
+  hipLaunchKernelGGL(moe_down, dim3((unsigned)blocks), dim3(p8::THREADS), p8::LDS_BYTES, stream,
                      reinterpret_cast<const _Float16*>(act), sorted_ids, offsets, topk_weights, W2,
                      reinterpret_cast<const _Float16*>(S2), Z2, reinterpret_cast<_Float16*>(Y), (int)pairs,
                      (int)experts, (int)H, (int)I, (int)group, (int)tiles_n);
