@@ -614,18 +614,24 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
   // DMA of step ks into stage st (out-of-range offsets past the last step:
   // nothing is read, the stage is not used again).
   // DMA instruction d (0 .. 8) of step ks into stage st
+  // past the last step the DMAs read through an empty resource (zeros, no
+  // traffic): a scalar select instead of a per-lane one
+  auto live_rsrc = [](bool live, i32x4 r) __attribute__((always_inline)) {
+    r[2] = __builtin_amdgcn_readfirstlane(live ? r[2] : 0);
+    return r;
+  };
   auto issue_one = [&](int ks, int st, int d) __attribute__((always_inline)) {
     const bool live = ks < nk;
     const uint32_t sb = lds0 + (uint32_t)(st * STAGE);
     if (d < AI) {
-      dma16(sb + (uint32_t)(8 * (AI * w + d) * 128), live ? a_off[d] : OOB, ra, (uint32_t)(ks * BK) * 2u);
+      dma16(sb + (uint32_t)(8 * (AI * w + d) * 128), a_off[d], live_rsrc(live, ra), (uint32_t)(ks * BK) * 2u);
     } else if (d < AI + 4) {
-      dma4(sb + (uint32_t)(A_ST + (8 * w + 2 * (d - AI)) * 128), live ? w_off[d - AI] : OOB, rw,
+      dma4(sb + (uint32_t)(A_ST + (8 * w + 2 * (d - AI)) * 128), w_off[d - AI], live_rsrc(live, rw),
            (uint32_t)(ks * BK) * half_n);
     } else {
       const uint32_t g = (uint32_t)(ks * BK) / (uint32_t)group;
       const uint32_t ss = w == 2 ? g * half_n : g * (uint32_t)N * 2u;
-      dma4(sb + (uint32_t)A_ST + sz_lds, live ? sz_off : OOB, rsz, ss);
+      dma4(sb + (uint32_t)A_ST + sz_lds, sz_off, live_rsrc(live, rsz), ss);
     }
   };
   auto issue = [&](int ks, int st) __attribute__((always_inline)) {
@@ -633,13 +639,13 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
     const uint32_t sb = lds0 + (uint32_t)(st * STAGE);
     const uint32_t sa = (uint32_t)(ks * BK) * 2u;
 #pragma unroll
-    for (int i = 0; i < AI; ++i) dma16(sb + (uint32_t)(8 * (AI * w + i) * 128), live ? a_off[i] : OOB, ra, sa);
+    for (int i = 0; i < AI; ++i) dma16(sb + (uint32_t)(8 * (AI * w + i) * 128), a_off[i], live_rsrc(live, ra), sa);
     const uint32_t sw = (uint32_t)(ks * BK) * half_n;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma4(sb + (uint32_t)(A_ST + (8 * w + 2 * i) * 128), live ? w_off[i] : OOB, rw, sw);
+    for (int i = 0; i < 4; ++i) dma4(sb + (uint32_t)(A_ST + (8 * w + 2 * i) * 128), w_off[i], live_rsrc(live, rw), sw);
     const uint32_t g = (uint32_t)(ks * BK) / (uint32_t)group;
     const uint32_t ss = w == 2 ? g * half_n : g * (uint32_t)N * 2u;
-    dma4(sb + (uint32_t)A_ST + sz_lds, live ? sz_off : OOB, rsz, ss);
+    dma4(sb + (uint32_t)A_ST + sz_lds, sz_off, live_rsrc(live, rsz), ss);
   };
 
   // A fragment mb of slice c: row 32 (MB wm + mb) + j, chunk 2c + h; its
