@@ -3,10 +3,12 @@
 // A is fp16 row-major; W is int4 in the N-packed, low-nibble-first layout with
 // group-wise fp16 scales and int4 zero-points along K (see include/tbhip.h).
 //
-// Dense prefill (w4a16_prefill, MFMA-bound for large M): one 256 x 256 output
-// tile per 512-thread block, eight wavefronts (two per SIMD); wavefront
-// (wm, wn) owns rows 128 wm .. +127 and columns 64 wn .. +63 as 4 x 2
-// v_mfma_f32_32x32x16_f16 accumulators.  Its two 32-column fragments are the
+// Prefill (MFMA-bound for large M): one 256 x 256 output tile per block.  The
+// dense kernel (w4a16_prefill) runs four wavefronts, one per SIMD, wavefront
+// w owning all rows and columns 64 w .. +63 as 8 x 2 v_mfma_f32_32x32x16_f16
+// accumulators (tile4); the grouped and MoE kernels run eight, two per SIMD,
+// wavefront (wm, wn) owning rows 128 wm .. +127 and columns 64 wn .. +63 as
+// 4 x 2 accumulators (tile8).  A wavefront's two 32-column fragments are the
 // even and the odd columns of its range: lane l owns packed byte l % 32 of
 // the range, so one byte per K row carries both of its columns.
 //
@@ -21,9 +23,9 @@
 //           standalone dequantiser's exact arithmetic ((1024 + q) and (64 + q)
 //           half2 from the 0x64 / 0x54 magic numbers, exact zero-point
 //           subtraction, one RNE multiply by the scale);
-//   MFMA  : while the 8 MFMAs of one slice run, the wavefront reads and
-//           dequantises the next slice; the DMA of step k + 3 is issued
-//           between the MFMAs that follow the step's barrier;
+//   MFMA  : while the MFMAs of one slice run (16 in tile4, 8 in tile8), the
+//           wavefront reads and dequantises the next slice; the DMA of step
+//           k + 3 is issued between the MFMAs that follow the step's barrier;
 //   output: each lane holds 8 consecutive columns of one row per accumulator
 //           group (even and odd accumulators interleaved): 16-byte stores
 //           straight from the accumulators.
@@ -33,7 +35,7 @@
 //           whole rounds more evenly.
 // The grouped GEMM (w4a16_grouped) and the MoE layer's gate/up (moe_gate_up:
 // gathered token rows, SiLU(gate) * up epilogue) and down (moe_down: routing
-// weight and scatter epilogue) projections run the same tile on each expert's
+// weight and scatter epilogue) projections run tile8 on each expert's
 // operands; a last column tile of at most 128 columns runs it as 256 x 128
 // (the eight wavefronts as 4 row groups x 2 column groups).  Every output
 // element sees the same MFMA operands in the same K order in all of them, so
@@ -884,12 +886,271 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
     }
   }
 }
+// Dense-prefill tile, four wavefronts (one per SIMD): 32 MB rows (MB = 8: 256,
+// MB = 6: 192) x 256 columns; wavefront w owns all rows and columns 64 w ..
+// 64 w + 63 as MB x 2 accumulators (up to 256 accumulator registers), so each
+// W fragment is dequantised once per block rather than by the two wavefronts
+// that share it in tile8 (half the VALU work, and under the power cap a
+// higher clock).  A lone wavefront cannot hide its own stalls behind another
+// one, so every operation of the next slice is placed between this slice's
+// MFMAs: the A fragments one after each of the first MB MFMAs, and each k-row
+// pair's dequantisation as three stages (and-or, subtract, multiply) one MFMA
+// apart, each pinned in place (the compiler would otherwise sink them to the
+// slice's end, where they stall the next slice's first MFMA).  Same LDS
+// stages, DMA, fragment layout and MFMA operands as tile8, so the results are
+// bit-identical to it.
+template <int MB>
+__device__ __forceinline__ void tile4(uint8_t* __restrict__ lds, const _Float16* __restrict__ A,
+                                      const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
+                                      const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int M, int N, int K,
+                                      int group, const Tile tile) {
+  static_assert(MB == 8 || MB == 6, "tile4 shapes");
+  constexpr int TM = 32 * MB;
+  constexpr int AI = TM / 32;  // A DMA instructions per wavefront and step (8 rows each, 4 wavefronts)
+  constexpr int WI = 8;        // W DMA instructions per wavefront and step (2 rows each)
+  constexpr int DMA_PER_STEP = AI + WI + 1;
+  constexpr int NQ = 2 * MB;   // MFMAs per slice
+  const int t = threadIdx.x, lane = t & 63, h = lane >> 5, j = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wn = w;
+  const int nk = K / BK;
+  const uint32_t half_n = (uint32_t)(N / 2);
+
+  const i32x4 ra = rsrc4(A, (uint32_t)M * (uint32_t)K * 2u);
+  const i32x4 rw = rsrc4(W, (uint32_t)K * half_n);
+  const i32x4 rs = rsrc4(S, (uint32_t)(K / group) * (uint32_t)N * 2u);
+  const i32x4 rz = rsrc4(Z, (uint32_t)(K / group) * half_n);
+  // past the last step the DMAs go through empty resources (zeros, no traffic)
+  auto live_rsrc = [](bool live, i32x4 r) __attribute__((always_inline)) {
+    r[2] = __builtin_amdgcn_readfirstlane(live ? r[2] : 0);
+    return r;
+  };
+
+  // A DMA: instruction i of wavefront w fills rows 8 (AI w + i) .. +7
+  uint32_t a_off[AI];
+#pragma unroll
+  for (int i = 0; i < AI; ++i) {
+    const int row = 8 * (AI * w + i) + (lane >> 3);
+    const int c = (lane & 7) ^ ((row ^ (row >> 3)) & 7);
+    const int m = tile.m0 + row;
+    a_off[i] = m < M ? ((uint32_t)m * (uint32_t)K + (uint32_t)c * 8u) * 2u : OOB;
+  }
+  // W DMA: instruction i of wavefront w fills rows 16 w + 2 i, +1 (lane L: row
+  // + L / 32, dword L % 32, 16-byte slot (L % 32) / 4 holding chunk slot ^ (row & 7))
+  uint32_t w_off[WI];
+#pragma unroll
+  for (int i = 0; i < WI; ++i) {
+    const int r = 16 * w + 2 * i + (lane >> 5);
+    const int c = ((lane & 31) >> 2) ^ (r & 7);
+    const uint32_t col = (uint32_t)(tile.n0 / 2 + c * 16 + (lane & 3) * 4);
+    w_off[i] = col < half_n ? (uint32_t)r * half_n + col : OOB;
+  }
+  uint32_t sz_off = OOB, sz_lds = PAD_OFF;
+  const bool zw = w == 2;
+  if (w < 2) {
+    const uint32_t col = (uint32_t)tile.n0 + (uint32_t)(w * 128 + lane * 2);
+    sz_off = col < (uint32_t)N ? col * 2u : OOB;
+    sz_lds = S_OFF + w * 256;
+  } else if (w == 2) {
+    const uint32_t col = (uint32_t)(tile.n0 / 2 + lane * 4);
+    sz_off = lane < 32 && col < half_n ? col : OOB;
+    sz_lds = Z_OFF;
+  }
+  const uint32_t lds0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)(
+      __attribute__((address_space(3))) void*)lds);
+
+  auto issue_one = [&](int ks, int st, int d) __attribute__((always_inline)) {
+    const bool live = ks < nk;
+    const uint32_t sb = lds0 + (uint32_t)(st * STAGE);
+    if (d < AI) {
+      dma16(sb + (uint32_t)(8 * (AI * w + d) * 128), a_off[d], live_rsrc(live, ra), (uint32_t)(ks * BK) * 2u);
+    } else if (d < AI + WI) {
+      dma4(sb + (uint32_t)(A_ST + (16 * w + 2 * (d - AI)) * 128), w_off[d - AI], live_rsrc(live, rw),
+           (uint32_t)(ks * BK) * half_n);
+    } else {
+      const uint32_t g = (uint32_t)(ks * BK) / (uint32_t)group;
+      const uint32_t ss = zw ? g * half_n : g * (uint32_t)N * 2u;
+      dma4(sb + (uint32_t)A_ST + sz_lds, sz_off, live_rsrc(live, zw ? rz : rs), ss);
+    }
+  };
+
+  uint32_t fa_off[4][2];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+      const int sw = (j ^ (4 * par + (j >> 3))) & 7;
+      fa_off[c][par] = (uint32_t)(j * 128 + (((2 * c + h) ^ sw) << 4));
+    }
+  uint32_t wt_off;
+  {
+    const int p = lane & 15, r = p >> 1, b = p & 1, G = lane >> 4;
+    const int pr = (r & 4) | ((r & 1) << 1) | ((r >> 1) & 1);
+    const int cb = 2 * wn + (G & 1);
+    wt_off = (uint32_t)(A_ST + (8 * (G >> 1) + pr) * 128 + ((cb ^ pr) << 4) + 8 * b);
+  }
+
+  f32x16 acc[MB][2];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) acc[i][0] = acc[i][1] = f32x16{};
+
+  const uint32_t c64 = __builtin_amdgcn_readfirstlane(0x64006400u) + (uint32_t)(lane >> 6);
+  const uint32_t c54 = __builtin_amdgcn_readfirstlane(0x54005400u) + (uint32_t)(lane >> 6);
+  h8 fa[2][MB];
+  h8 wf[2][2];
+  uint32_t sE = 0, sO = 0, zE = 0, zO = 0;
+
+  auto load_scales = [&](int st) __attribute__((always_inline)) {
+    const uint8_t* sb = lds + st * STAGE + A_ST;
+    const uint32_t s2 = *reinterpret_cast<const uint32_t*>(sb + S_OFF + (wn * 64 + 2 * j) * 2);
+    const uint32_t zb = sb[Z_OFF + wn * 32 + j];
+    sE = perm(s2, s2, 0x01000100u);
+    sO = perm(s2, s2, 0x03020302u);
+    const uint32_t zz = zb | (zb << 16);
+    zE = (zz & 0x000F000Fu) | 0x64006400u;
+    zO = (zz & 0x00F000F0u) | 0x54005400u;
+  };
+  auto read_a = [&](int st, int c, int buf, int mb) __attribute__((always_inline)) {
+    typedef __attribute__((address_space(3))) uint8_t lds_u8;
+    lds_u8* const base = (lds_u8*)(__attribute__((address_space(3))) void*)lds;
+    fa[buf][mb] = *(__attribute__((address_space(3))) const h8*)(base + fa_off[c][mb & 1] +
+                                                                   (st * STAGE + mb * 4096));
+  };
+  auto read_w = [&](int st, int c) __attribute__((always_inline)) -> v2i {
+    typedef __attribute__((address_space(3))) uint8_t lds_u8;
+    lds_u8* const base = (lds_u8*)(__attribute__((address_space(3))) void*)lds;
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+        (__attribute__((address_space(3))) v2i*)(base + st * STAGE + c * 2048 + wt_off));
+  };
+  auto dequant_pair = [&](const v2i x, int q, u32x4& e, u32x4& o) __attribute__((always_inline)) {
+    const uint32_t src = (uint32_t)x[q >> 1];
+    const uint32_t d = (q & 1) ? src >> 8 : src;
+    e[q] = as_u32((as_h2(and_or(d, 0x000F000Fu, c64)) - as_h2(zE)) * as_h2(sE));
+    o[q] = as_u32((as_h2(and_or(d, 0x00F000F0u, c54)) - as_h2(zO)) * as_h2(sO));
+  };
+
+  constexpr int VM1 = DMA_PER_STEP, VM2 = 2 * DMA_PER_STEP;
+  constexpr int WAIT_BAR = (VM1 & 15) | ((VM1 >> 4) << 14) | (7 << 4) | (0 << 8);
+  constexpr int WAIT_PRO = (VM2 & 15) | ((VM2 >> 4) << 14) | (7 << 4) | (0 << 8);
+  auto barrier = [&]() __attribute__((always_inline)) {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+#pragma unroll
+  for (int st = 0; st < 3; ++st)
+#pragma unroll
+    for (int d = 0; d < DMA_PER_STEP; ++d) issue_one(st, st, d);
+  __builtin_amdgcn_s_waitcnt(WAIT_PRO);
+  barrier();
+  load_scales(0);
+  v2i xs[4];
+  {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) xs[c] = read_w(0, c);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) read_a(0, 0, 0, mb);
+    u32x4 e, o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dequant_pair(xs[0], q, e, o);
+    wf[0][0] = __builtin_bit_cast(h8, e);
+    wf[0][1] = __builtin_bit_cast(h8, o);
+  }
+
+  // One k16 slice: 2 MB MFMAs on buffer `cur`, one operation of the next
+  // slice after each: its A fragments first, its dequantisation (one k-row
+  // pair every other MFMA) last.  The slice after a barrier (cn == 0) also
+  // reads the byte columns of the new stage's four slices.
+  auto slice = [&](int cur, int nst, int cn, auto body) __attribute__((always_inline)) {
+    u32x4 e, o;
+    uint32_t ae[4], ao[4], se[4], so[4];
+    // k-row pair p's dequantisation in three pinned stages one MFMA apart:
+    // and-or at slot SA + 2p, subtract at SA + 2p + 1, multiply at SA + 2p + 2
+    constexpr int SA = NQ - 10;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int mb = q >> 1, nb = q & 1;
+      acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[cur][nb], fa[cur][mb], acc[mb][nb], 0, 0, 0);
+      if (cn == 0 && q == 0) xs[0] = read_w(nst, 0);
+      if (q >= 1 && q <= MB) read_a(nst, cn, cur ^ 1, q - 1);
+      if (cn == 0 && q >= MB + 1 && q <= MB + 3) xs[q - MB] = read_w(nst, q - MB);
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        if (q == SA + 2 * pp) {
+          const uint32_t src = (uint32_t)xs[cn][pp >> 1];
+          const uint32_t d = (pp & 1) ? src >> 8 : src;
+          ae[pp] = and_or(d, 0x000F000Fu, c64);
+          ao[pp] = and_or(d, 0x00F000F0u, c54);
+          asm volatile("" : "+v"(ae[pp]), "+v"(ao[pp]));
+        }
+        if (q == SA + 2 * pp + 1) {
+          se[pp] = as_u32(as_h2(ae[pp]) - as_h2(zE));
+          so[pp] = as_u32(as_h2(ao[pp]) - as_h2(zO));
+          asm volatile("" : "+v"(se[pp]), "+v"(so[pp]));
+        }
+        if (q == SA + 2 * pp + 2) {
+          e[pp] = as_u32(as_h2(se[pp]) * as_h2(sE));
+          o[pp] = as_u32(as_h2(so[pp]) * as_h2(sO));
+          asm volatile("" : "+v"(e[pp]), "+v"(o[pp]));
+        }
+      }
+      body(q);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    wf[cur ^ 1][0] = __builtin_bit_cast(h8, e);
+    wf[cur ^ 1][1] = __builtin_bit_cast(h8, o);
+  };
+  auto none = [](int) {};
+
+  auto step = [&](int kt, auto stc) __attribute__((always_inline)) {
+    constexpr int ST = decltype(stc)::value;
+    constexpr int NST = (ST + 1) % 3;
+    slice(0, ST, 1, none);
+    slice(1, ST, 2, none);
+    slice(0, ST, 3, none);
+    __builtin_amdgcn_s_waitcnt(WAIT_BAR);
+    barrier();
+    load_scales(NST);
+    slice(1, NST, 0, [&](int q) {
+      issue_one(kt + 3, ST, q);
+      if (q == NQ - 1) {
+#pragma unroll
+        for (int d = NQ; d < DMA_PER_STEP; ++d) issue_one(kt + 3, ST, d);
+      }
+    });
+  };
+  int kt = 0;
+  for (; kt + 2 < nk; kt += 3) {
+    step(kt, std::integral_constant<int, 0>{});
+    step(kt + 1, std::integral_constant<int, 1>{});
+    step(kt + 2, std::integral_constant<int, 2>{});
+  }
+  if (kt < nk) step(kt, std::integral_constant<int, 0>{});
+  if (kt + 1 < nk) step(kt + 1, std::integral_constant<int, 1>{});
+  __builtin_amdgcn_s_waitcnt(0);
+
+  const int col0 = tile.n0 + 64 * wn + 8 * h;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int m = tile.m0 + 32 * mb + j;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int n = col0 + 16 * g;
+      u32x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        v[e] = as_u32(f16x2{(_Float16)acc[mb][0][4 * g + e], (_Float16)acc[mb][1][4 * g + e]});
+      if (m < M && n < N) *reinterpret_cast<u32x4*>(Y + (int64_t)m * N + n) = v;
+    }
+  }
+}
 }  // namespace p8
 
 // Blocks [0, n_full) take 256-row tiles of columns [0, 256 n_split); blocks
 // n_full .. take 192-row tiles of the remaining columns.  Each part is
 // numbered XCD-aware on its own (both start at a multiple of 8 blocks).
-__global__ void __launch_bounds__(p8::THREADS, 1)
+__global__ void __launch_bounds__(256, 1)
     w4a16_prefill(const _Float16* __restrict__ A, const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
                    const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int M, int N, int K, int group,
                    int tiles_m, int n_split, int n_full, int tail_m, int tail_n, int tail_blocks) {
@@ -897,13 +1158,13 @@ __global__ void __launch_bounds__(p8::THREADS, 1)
   uint8_t* const lds = reinterpret_cast<uint8_t*>(lds_h);
   const int b = blockIdx.x;
   if (b < n_full) {
-    p8::tile8<4>(lds, A, W, S, Z, Y, M, N, K, group, p8::tile_of(b, n_full, tiles_m, n_split, 256, 0));
+    p8::tile4<8>(lds, A, W, S, Z, Y, M, N, K, group, p8::tile_of(b, n_full, tiles_m, n_split, 256, 0));
   } else {
     const int tb = b - n_full;
     const int n_tail = tail_m * tail_n;
     const int idx = p8::remap_xcd(tb, tail_blocks);
     if (idx >= n_tail) return;
-    p8::tile8<3>(lds, A, W, S, Z, Y, M, N, K, group, p8::tile_in_grid(idx, tail_m, tail_n, 192, n_split * BN));
+    p8::tile4<6>(lds, A, W, S, Z, Y, M, N, K, group, p8::tile_in_grid(idx, tail_m, tail_n, 192, n_split * BN));
   }
 }
 
@@ -1114,7 +1375,7 @@ static tb_status launch_dense(const char* fn, const uint16_t* A, const uint8_t* 
   if (tb_status st = tb::reserve_lds(reinterpret_cast<const void*>(&w4a16_prefill), p8::LDS_BYTES, fn)) return st;
   const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
   const PrefillPlan pl = plan_prefill((int)M, tiles_m, tiles_n, device_cus());
-  hipLaunchKernelGGL(w4a16_prefill, dim3(pl.n_full + pl.tail_blocks), dim3(p8::THREADS), p8::LDS_BYTES, stream,
+  hipLaunchKernelGGL(w4a16_prefill, dim3(pl.n_full + pl.tail_blocks), dim3(256), p8::LDS_BYTES, stream,
                      reinterpret_cast<const _Float16*>(A), W, reinterpret_cast<const _Float16*>(scales), zeros,
                      reinterpret_cast<_Float16*>(Y), (int)M, (int)N, (int)K, (int)group, tiles_m, pl.n_split,
                      pl.n_full, pl.tail_m, pl.tail_n, pl.tail_blocks);
