@@ -4,13 +4,15 @@
 // group-wise fp16 scales and int4 zero-points along K (see include/tbhip.h).
 //
 // Prefill (MFMA-bound for large M): one 256 x 256 output tile per block.  The
-// dense kernel (w4a16_prefill) runs four wavefronts, one per SIMD, wavefront
-// w owning all rows and columns 64 w .. +63 as 8 x 2 v_mfma_f32_32x32x16_f16
-// accumulators (tile4); the grouped and MoE kernels run eight, two per SIMD,
-// wavefront (wm, wn) owning rows 128 wm .. +127 and columns 64 wn .. +63 as
-// 4 x 2 accumulators (tile8).  A wavefront's two 32-column fragments are the
-// even and the odd columns of its range: lane l owns packed byte l % 32 of
-// the range, so one byte per K row carries both of its columns.
+// dense, grouped and MoE gate/up kernels run four wavefronts, one per SIMD,
+// wavefront w owning all rows and columns 64 w .. +63 as 8 x 2
+// v_mfma_f32_32x32x16_f16 accumulators (tile4); the MoE down projection
+// (K = I, a few K steps per tile) runs eight, two per SIMD, wavefront
+// (wm, wn) owning rows 128 wm .. +127 and columns 64 wn .. +63 as 4 x 2
+// accumulators (tile8), whose second wavefront per SIMD hides its short
+// tiles' prologue and scatter epilogue.  A wavefront's two 32-column
+// fragments are the even and the odd columns of its range: lane l owns packed
+// byte l % 32 of the range, so one byte per K row carries both of its columns.
 //
 //   A, W  : the A tile ([256][64 halfs]), the packed W tile ([64][128 B]) and
 //           the step's group of scales and zero-points stream HBM -> LDS by
@@ -35,11 +37,11 @@
 //           whole rounds more evenly.
 // The grouped GEMM (w4a16_grouped) and the MoE layer's gate/up (moe_gate_up:
 // gathered token rows, SiLU(gate) * up epilogue) and down (moe_down: routing
-// weight and scatter epilogue) projections run tile8 on each expert's
-// operands; a last column tile of at most 128 columns runs it as 256 x 128
-// (the eight wavefronts as 4 row groups x 2 column groups).  Every output
-// element sees the same MFMA operands in the same K order in all of them, so
-// an expert's rows equal the dense product bit for bit.
+// weight and scatter epilogue) projections run the tile on each expert's
+// operands; a last column tile of at most 128 columns runs as 256 x 128 (the
+// wavefronts as 2 row groups x 2 column groups in tile4, 4 x 2 in tile8).
+// Every output element sees the same MFMA operands in the same K order in
+// all of them, so an expert's rows equal the dense product bit for bit.
 //
 // Tiles are numbered XCD-aware: consecutive hardware block ids land on
 // different XCDs, so block ids are first regrouped so that each XCD owns a
@@ -886,12 +888,14 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
     }
   }
 }
-// Dense-prefill tile, four wavefronts (one per SIMD): 32 MB rows (MB = 8: 256,
-// MB = 6: 192) x 256 columns; wavefront w owns all rows and columns 64 w ..
-// 64 w + 63 as MB x 2 accumulators (up to 256 accumulator registers), so each
-// W fragment is dequantised once per block rather than by the two wavefronts
-// that share it in tile8 (half the VALU work, and under the power cap a
-// higher clock).  A lone wavefront cannot hide its own stalls behind another
+// Four-wavefront tile (one wavefront per SIMD).  WN = 4: 32 MB rows (MB = 8:
+// 256, MB = 6: 192) x 256 columns, wavefront w owning all rows and columns
+// 64 w .. 64 w + 63 as MB x 2 accumulators (up to 256 accumulator
+// registers), so each W fragment is dequantised once per block rather than by
+// the two wavefronts that share it in tile8 (half the VALU work, and under
+// the power cap a higher clock).  WN = 2, MB = 4: 256 rows x 128 columns, the
+// wavefronts as 2 row groups x 2 column groups, for a last column tile of at
+// most 128 columns.  Modes, rows and a_rows as in tile8.  A lone wavefront cannot hide its own stalls behind another
 // one, so every operation of the next slice is placed between this slice's
 // MFMAs: the A fragments one after each of the first MB MFMAs, and each k-row
 // pair's dequantisation as three stages (and-or, subtract, multiply) one MFMA
@@ -899,24 +903,26 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
 // slice's end, where they stall the next slice's first MFMA).  Same LDS
 // stages, DMA, fragment layout and MFMA operands as tile8, so the results are
 // bit-identical to it.
-template <int MB>
+template <int MB, int WN = 4, int MODE = T_PLAIN>
 __device__ __forceinline__ void tile4(uint8_t* __restrict__ lds, const _Float16* __restrict__ A,
                                       const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
                                       const uint8_t* __restrict__ Z, _Float16* __restrict__ Y, int M, int N, int K,
-                                      int group, const Tile tile) {
-  static_assert(MB == 8 || MB == 6, "tile4 shapes");
-  constexpr int TM = 32 * MB;
+                                      int group, const Tile tile, int a_rows = -1, const RowMap rm = RowMap{}) {
+  static_assert((WN == 4 && (MB == 8 || MB == 6)) || (WN == 2 && MB == 4), "tile4 shapes");
+  if (MODE == T_PLAIN) a_rows = M;
+  constexpr int TM = 32 * MB * (4 / WN);  // tile rows
   constexpr int AI = TM / 32;  // A DMA instructions per wavefront and step (8 rows each, 4 wavefronts)
   constexpr int WI = 8;        // W DMA instructions per wavefront and step (2 rows each)
   constexpr int DMA_PER_STEP = AI + WI + 1;
   constexpr int NQ = 2 * MB;   // MFMAs per slice
   const int t = threadIdx.x, lane = t & 63, h = lane >> 5, j = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int wn = w;
+  const int wm = w / WN, wn = w % WN;
   const int nk = K / BK;
   const uint32_t half_n = (uint32_t)(N / 2);
+  const int I = N / 2, a0 = tile.n0 / 2;  // T_GATE_UP: activation columns
 
-  const i32x4 ra = rsrc4(A, (uint32_t)M * (uint32_t)K * 2u);
+  const i32x4 ra = rsrc4(A, (uint32_t)a_rows * (uint32_t)K * 2u);
   const i32x4 rw = rsrc4(W, (uint32_t)K * half_n);
   const i32x4 rs = rsrc4(S, (uint32_t)(K / group) * (uint32_t)N * 2u);
   const i32x4 rz = rsrc4(Z, (uint32_t)(K / group) * half_n);
@@ -933,7 +939,12 @@ __device__ __forceinline__ void tile4(uint8_t* __restrict__ lds, const _Float16*
     const int row = 8 * (AI * w + i) + (lane >> 3);
     const int c = (lane & 7) ^ ((row ^ (row >> 3)) & 7);
     const int m = tile.m0 + row;
-    a_off[i] = m < M ? ((uint32_t)m * (uint32_t)K + (uint32_t)c * 8u) * 2u : OOB;
+    int src = m;
+    if (MODE == T_GATE_UP && m < M) {
+      const int pid = rm.ids[m];
+      src = (unsigned)pid < (unsigned)rm.pairs ? pid / rm.topk : a_rows;
+    }
+    a_off[i] = m < M && src < a_rows ? ((uint32_t)src * (uint32_t)K + (uint32_t)c * 8u) * 2u : OOB;
   }
   // W DMA: instruction i of wavefront w fills rows 16 w + 2 i, +1 (lane L: row
   // + L / 32, dword L % 32, 16-byte slot (L % 32) / 4 holding chunk slot ^ (row & 7))
@@ -942,18 +953,40 @@ __device__ __forceinline__ void tile4(uint8_t* __restrict__ lds, const _Float16*
   for (int i = 0; i < WI; ++i) {
     const int r = 16 * w + 2 * i + (lane >> 5);
     const int c = ((lane & 31) >> 2) ^ (r & 7);
-    const uint32_t col = (uint32_t)(tile.n0 / 2 + c * 16 + (lane & 3) * 4);
-    w_off[i] = col < half_n ? (uint32_t)r * half_n + col : OOB;
+    if (MODE == T_GATE_UP) {
+      // chunk c: gate (c even) or up (c odd) of activation columns a0 + 32 (c / 2) ..,
+      // this dword their 8 columns from a0 + 32 (c / 2) + 8 (lane % 4)
+      const int acol = a0 + 32 * (c >> 1) + 8 * (lane & 3);
+      const uint32_t byte = (uint32_t)((c & 1) * (I / 2) + acol / 2);
+      w_off[i] = acol < I ? (uint32_t)r * half_n + byte : OOB;
+    } else {
+      const uint32_t col = (uint32_t)(tile.n0 / 2 + c * 16 + (lane & 3) * 4);
+      w_off[i] = col < half_n ? (uint32_t)r * half_n + col : OOB;
+    }
   }
   uint32_t sz_off = OOB, sz_lds = PAD_OFF;
   const bool zw = w == 2;
   if (w < 2) {
-    const uint32_t col = (uint32_t)tile.n0 + (uint32_t)(w * 128 + lane * 2);
-    sz_off = col < (uint32_t)N ? col * 2u : OOB;
+    if (MODE == T_GATE_UP) {
+      // scale slot t = 128 w + 2 lane (two columns) of column group t / 64:
+      // gate (t % 64 < 32) or up of activation column a0 + 32 (t / 64) + t % 32
+      const int t2 = 128 * w + 2 * lane, acol = a0 + 32 * (t2 >> 6) + (t2 & 31);
+      sz_off = acol < I ? (uint32_t)(((t2 & 32) ? I : 0) + acol) * 2u : OOB;
+    } else {
+      const uint32_t col = (uint32_t)tile.n0 + (uint32_t)(w * 128 + lane * 2);
+      sz_off = col < (uint32_t)N ? col * 2u : OOB;
+    }
     sz_lds = S_OFF + w * 256;
   } else if (w == 2) {
-    const uint32_t col = (uint32_t)(tile.n0 / 2 + lane * 4);
-    sz_off = lane < 32 && col < half_n ? col : OOB;
+    if (MODE == T_GATE_UP) {
+      // zero-point bytes b = 4 lane .. + 3 of column group b / 32: gate
+      // (b % 32 < 16) or up bytes of activation columns a0 + 32 (b / 32) + 2 (b % 16) ..
+      const int b = 4 * lane, acol = a0 + 32 * (b >> 5) + 2 * (b & 15);
+      sz_off = lane < 32 && acol < I ? (uint32_t)(((b & 16) ? I / 2 : 0) + acol / 2) : OOB;
+    } else {
+      const uint32_t col = (uint32_t)(tile.n0 / 2 + lane * 4);
+      sz_off = lane < 32 && col < half_n ? col : OOB;
+    }
     sz_lds = Z_OFF;
   }
   const uint32_t lds0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)(
@@ -980,7 +1013,7 @@ __device__ __forceinline__ void tile4(uint8_t* __restrict__ lds, const _Float16*
 #pragma unroll
     for (int par = 0; par < 2; ++par) {
       const int sw = (j ^ (4 * par + (j >> 3))) & 7;
-      fa_off[c][par] = (uint32_t)(j * 128 + (((2 * c + h) ^ sw) << 4));
+      fa_off[c][par] = (uint32_t)(wm * MB * 4096 + j * 128 + (((2 * c + h) ^ sw) << 4));
     }
   uint32_t wt_off;
   {
@@ -993,6 +1026,18 @@ __device__ __forceinline__ void tile4(uint8_t* __restrict__ lds, const _Float16*
   f32x16 acc[MB][2];
 #pragma unroll
   for (int i = 0; i < MB; ++i) acc[i][0] = acc[i][1] = f32x16{};
+
+  // T_DOWN: the pair id of each of the lane's rows now, its routing weight
+  // after the prologue, so that neither load's latency lands in the epilogue
+  int row_pid[MODE == T_DOWN ? MB : 1];
+  float row_w[MODE == T_DOWN ? MB : 1];
+  if (MODE == T_DOWN) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int m = tile.m0 + 32 * (MB * wm + mb) + j;
+      row_pid[mb] = m < M ? rm.ids[m] : -1;
+    }
+  }
 
   const uint32_t c64 = __builtin_amdgcn_readfirstlane(0x64006400u) + (uint32_t)(lane >> 6);
   const uint32_t c54 = __builtin_amdgcn_readfirstlane(0x54005400u) + (uint32_t)(lane >> 6);
@@ -1013,7 +1058,7 @@ __device__ __forceinline__ void tile4(uint8_t* __restrict__ lds, const _Float16*
   auto read_a = [&](int st, int c, int buf, int mb) __attribute__((always_inline)) {
     typedef __attribute__((address_space(3))) uint8_t lds_u8;
     lds_u8* const base = (lds_u8*)(__attribute__((address_space(3))) void*)lds;
-    fa[buf][mb] = *(__attribute__((address_space(3))) const h8*)(base + fa_off[c][mb & 1] +
+    fa[buf][mb] = *(__attribute__((address_space(3))) const h8*)(base + fa_off[c][(MB * wm + mb) & 1] +
                                                                    (st * STAGE + mb * 4096));
   };
   auto read_w = [&](int st, int c) __attribute__((always_inline)) -> v2i {
@@ -1045,6 +1090,11 @@ __device__ __forceinline__ void tile4(uint8_t* __restrict__ lds, const _Float16*
   __builtin_amdgcn_s_waitcnt(WAIT_PRO);
   barrier();
   load_scales(0);
+  if (MODE == T_DOWN) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+      row_w[mb] = (unsigned)row_pid[mb] < (unsigned)rm.pairs ? rm.w[row_pid[mb]] : 0.f;
+  }
   v2i xs[4];
   {
 #pragma unroll
@@ -1066,8 +1116,8 @@ __device__ __forceinline__ void tile4(uint8_t* __restrict__ lds, const _Float16*
     u32x4 e, o;
     uint32_t ae[4], ao[4], se[4], so[4];
     // k-row pair p's dequantisation in three pinned stages one MFMA apart:
-    // and-or at slot SA + 2p, subtract at SA + 2p + 1, multiply at SA + 2p + 2
-    constexpr int SA = NQ - 10;
+    // and-or at slot SA + SP p, subtract one slot later, multiply two slots later
+    constexpr int SA = NQ >= 12 ? NQ - 10 : 1, SP = NQ >= 12 ? 2 : 1;
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int mb = q >> 1, nb = q & 1;
@@ -1077,19 +1127,19 @@ __device__ __forceinline__ void tile4(uint8_t* __restrict__ lds, const _Float16*
       if (cn == 0 && q >= MB + 1 && q <= MB + 3) xs[q - MB] = read_w(nst, q - MB);
 #pragma unroll
       for (int pp = 0; pp < 4; ++pp) {
-        if (q == SA + 2 * pp) {
+        if (q == SA + SP * pp) {
           const uint32_t src = (uint32_t)xs[cn][pp >> 1];
           const uint32_t d = (pp & 1) ? src >> 8 : src;
           ae[pp] = and_or(d, 0x000F000Fu, c64);
           ao[pp] = and_or(d, 0x00F000F0u, c54);
           asm volatile("" : "+v"(ae[pp]), "+v"(ao[pp]));
         }
-        if (q == SA + 2 * pp + 1) {
+        if (q == SA + SP * pp + 1) {
           se[pp] = as_u32(as_h2(ae[pp]) - as_h2(zE));
           so[pp] = as_u32(as_h2(ao[pp]) - as_h2(zO));
           asm volatile("" : "+v"(se[pp]), "+v"(so[pp]));
         }
-        if (q == SA + 2 * pp + 2) {
+        if (q == SA + SP * pp + 2) {
           e[pp] = as_u32(as_h2(se[pp]) * as_h2(sE));
           o[pp] = as_u32(as_h2(so[pp]) * as_h2(sO));
           asm volatile("" : "+v"(e[pp]), "+v"(o[pp]));
@@ -1130,18 +1180,59 @@ __device__ __forceinline__ void tile4(uint8_t* __restrict__ lds, const _Float16*
   if (kt + 1 < nk) step(kt + 1, std::integral_constant<int, 1>{});
   __builtin_amdgcn_s_waitcnt(0);
 
+  // Epilogue: element 4g + e of accumulator (mb, nb) is row 32 (MB wm + mb) + j,
+  // column 64 wn + 16 g + 8 h + 2 e + nb of the tile.
+  if (MODE == T_GATE_UP) {
+    // g = 0, 1: gate of activation columns a0 + 32 wn + 16 g + 8 h + 2 e + nb;
+    // g + 2: up of the same columns
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int m = tile.m0 + 32 * (MB * wm + mb) + j;
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const int acol = a0 + 32 * wn + 16 * g + 8 * h;
+        u32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          _Float16 r[2];
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb) {
+            const float gv = (float)(_Float16)acc[mb][nb][4 * g + e];
+            const float uv = (float)(_Float16)acc[mb][nb][4 * (g + 2) + e];
+            float sg = 1.0f + expf(-gv);
+            asm volatile("" : "+v"(sg));
+            r[nb] = h_of_rounded(gv / sg * uv);
+          }
+          v[e] = as_u32(f16x2{r[0], r[1]});
+        }
+        if (m < M && acol < I) *reinterpret_cast<u32x4*>(Y + (int64_t)m * I + acol) = v;
+      }
+    }
+    return;
+  }
   const int col0 = tile.n0 + 64 * wn + 8 * h;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
-    const int m = tile.m0 + 32 * mb + j;
+    const int m = tile.m0 + 32 * (MB * wm + mb) + j;
+    int64_t dst = m;
+    float rw = 1.f;
+    if (MODE == T_DOWN) {
+      dst = row_pid[mb];
+      rw = row_w[mb];
+    }
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int n = col0 + 16 * g;
       u32x4 v;
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        v[e] = as_u32(f16x2{(_Float16)acc[mb][0][4 * g + e], (_Float16)acc[mb][1][4 * g + e]});
-      if (m < M && n < N) *reinterpret_cast<u32x4*>(Y + (int64_t)m * N + n) = v;
+      for (int e = 0; e < 4; ++e) {
+        if (MODE == T_DOWN)
+          v[e] = as_u32(f16x2{h_of_rounded(acc[mb][0][4 * g + e] * rw), h_of_rounded(acc[mb][1][4 * g + e] * rw)});
+        else
+          v[e] = as_u32(f16x2{(_Float16)acc[mb][0][4 * g + e], (_Float16)acc[mb][1][4 * g + e]});
+      }
+      const bool ok = MODE == T_DOWN ? (unsigned)dst < (unsigned)rm.pairs : m < M;
+      if (ok && n < N) *reinterpret_cast<u32x4*>(Y + dst * N + n) = v;
     }
   }
 }
@@ -1177,7 +1268,7 @@ __global__ void __launch_bounds__(256, 1)
 // is the dense kernel's 256 x 256 tile on the expert's operands, its A and Y
 // based at the tile's first row with the rows up to the expert's last as the
 // valid ones, so each expert segment equals the dense product bit for bit.
-__global__ void __launch_bounds__(p8::THREADS, 1)
+__global__ void __launch_bounds__(256, 1)
     w4a16_grouped(const _Float16* __restrict__ A, const uint8_t* __restrict__ W, const _Float16* __restrict__ S,
                   const uint8_t* __restrict__ Z, const int* __restrict__ offsets, _Float16* __restrict__ Y, int R,
                   int experts, int N, int K, int group, int tiles_n) {
@@ -1191,10 +1282,10 @@ __global__ void __launch_bounds__(p8::THREADS, 1)
   // a last column tile of at most 128 columns (N = 1408 is 5.5 tiles) runs
   // as 256 x 128: half the MFMAs, the same dequantisation per wavefront
   if (N - nt * BN <= BN / 2)
-    p8::tile8<2, 2>(lds, A + (int64_t)m0 * K, W + e * wstride, S + e * sstride, Z + e * zstride,
+    p8::tile4<4, 2>(lds, A + (int64_t)m0 * K, W + e * wstride, S + e * sstride, Z + e * zstride,
                     Y + (int64_t)m0 * N, m_end - m0, N, K, group, Tile{0, nt * BN});
   else
-    p8::tile8<4>(lds, A + (int64_t)m0 * K, W + e * wstride, S + e * sstride, Z + e * zstride, Y + (int64_t)m0 * N,
+    p8::tile4<8>(lds, A + (int64_t)m0 * K, W + e * wstride, S + e * sstride, Z + e * zstride, Y + (int64_t)m0 * N,
                  m_end - m0, N, K, group, Tile{0, nt * BN});
 }
 
@@ -1203,7 +1294,7 @@ __global__ void __launch_bounds__(p8::THREADS, 1)
 // topk], multiply by expert e's W13 [K, 2I] and write fp16(silu(gate) * up),
 // I columns per row, in the same sorted row order.  128 activation columns per
 // tile (64 for a last tile of at most 64: the 256 x 128 layout).
-__global__ void __launch_bounds__(p8::THREADS, 1)
+__global__ void __launch_bounds__(256, 1)
     moe_gate_up(const _Float16* __restrict__ X, const int* __restrict__ ids, const int* __restrict__ offsets,
                 const uint8_t* __restrict__ W, const _Float16* __restrict__ S, const uint8_t* __restrict__ Z,
                 _Float16* __restrict__ act, int tokens, int topk, int pairs, int experts, int I, int K, int group,
@@ -1221,10 +1312,10 @@ __global__ void __launch_bounds__(p8::THREADS, 1)
   rm.topk = topk;
   rm.pairs = pairs;
   if (I - nt * (BN / 2) <= BN / 4)
-    p8::tile8<2, 2, p8::T_GATE_UP>(lds, X, W + e * wstride, S + e * sstride, Z + e * zstride, act + (int64_t)m0 * I,
+    p8::tile4<4, 2, p8::T_GATE_UP>(lds, X, W + e * wstride, S + e * sstride, Z + e * zstride, act + (int64_t)m0 * I,
                                    m_end - m0, N, K, group, Tile{0, nt * BN}, tokens, rm);
   else
-    p8::tile8<4, 4, p8::T_GATE_UP>(lds, X, W + e * wstride, S + e * sstride, Z + e * zstride, act + (int64_t)m0 * I,
+    p8::tile4<8, 4, p8::T_GATE_UP>(lds, X, W + e * wstride, S + e * sstride, Z + e * zstride, act + (int64_t)m0 * I,
                                    m_end - m0, N, K, group, Tile{0, nt * BN}, tokens, rm);
 }
 
@@ -1502,7 +1593,7 @@ extern "C" tb_status tb_moe_w4a16_grouped_gemm(const uint16_t* A, const uint8_t*
   const int64_t tile_rows = (R + BM - 1) / BM + experts;  // upper bound on sum_e ceil(rows_e / 256)
   const int64_t blocks = tile_rows * tiles_n;
   TB_CHECK_ARG(blocks < (1ll << 31), "tb_moe_w4a16_grouped_gemm: problem too large");
-  hipLaunchKernelGGL(w4a16_grouped, dim3((unsigned)blocks), dim3(p8::THREADS), p8::LDS_BYTES, stream,
+  hipLaunchKernelGGL(w4a16_grouped, dim3((unsigned)blocks), dim3(256), p8::LDS_BYTES, stream,
                      reinterpret_cast<const _Float16*>(A), W, reinterpret_cast<const _Float16*>(scales), zeros, offsets,
                      reinterpret_cast<_Float16*>(Y), (int)R, (int)experts, (int)N, (int)K, (int)group, (int)tiles_n);
   return tb::launch_status("tb_moe_w4a16_grouped_gemm");
@@ -1536,7 +1627,7 @@ extern "C" tb_status tb_moe_w4a16_gate_up(const uint16_t* X, const int32_t* sort
   const int64_t tile_rows = (pairs + BM - 1) / BM + experts;
   const int64_t blocks = tile_rows * tiles_n;
   TB_CHECK_ARG(blocks < (1ll << 31), "%s: problem too large", fn);
-  hipLaunchKernelGGL(moe_gate_up, dim3((unsigned)blocks), dim3(p8::THREADS), p8::LDS_BYTES, stream,
+  hipLaunchKernelGGL(moe_gate_up, dim3((unsigned)blocks), dim3(256), p8::LDS_BYTES, stream,
                      reinterpret_cast<const _Float16*>(X), sorted_ids, offsets, W13,
                      reinterpret_cast<const _Float16*>(S13), Z13, reinterpret_cast<_Float16*>(act), (int)tokens,
                      (int)topk, (int)pairs, (int)experts, (int)I, (int)H, (int)group, (int)tiles_n);
