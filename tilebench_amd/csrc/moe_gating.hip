@@ -534,25 +534,17 @@ __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__
   if (__builtin_amdgcn_ballot_w64(!(finite && total <= 2 * LPR)) == 0) {
     // 4. compact the row's candidates into cand[slot], each as the exact
     // (key, 1023 - index) pair, so a lane reads its candidate in one step
-    int pos = incl - cnt;
-    auto put = [&](int j) {
-      const int idx = (j / EPC) * (LPR * EPC) + q * EPC + (j % EPC);
-      cand[slot][pos++] = ((uint64_t)key_of_bits(f[j]) << 32) | (uint32_t)(1023 - idx);
-    };
-    if constexpr (V <= 4) {
+    // (candidate j of the lane goes to its slot among the row's: the lane's
+    // base plus the candidates before it in the lane, a popcount, so the
+    // writes do not wait on one another)
+    const int base = incl - cnt;
 #pragma unroll
-      for (int j = 0; j < V; ++j)
-        if ((mask >> j) & 1u) put(j);
-    } else {
-      uint32_t mm = mask;
-      while (__builtin_amdgcn_ballot_w64(mm != 0)) {
-        if (mm != 0) {
-          const int j = __builtin_ctz(mm);
-          mm &= mm - 1;
-          put(j);
-        }
+    for (int j = 0; j < V; ++j)
+      if ((mask >> j) & 1u) {
+        const int idx = (j / EPC) * (LPR * EPC) + q * EPC + (j % EPC);
+        cand[slot][base + __builtin_popcount(mask & ((1u << j) - 1u))] =
+            ((uint64_t)key_of_bits(f[j]) << 32) | (uint32_t)(1023 - idx);
       }
-    }
     // The list is read by other lanes of this wavefront only (each wavefront
     // owns its rows' LDS), so a wavefront-scope fence orders the accesses.
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
