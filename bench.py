@@ -7,8 +7,9 @@
 A step is one launch of the operator on one batch of seeded synthetic input
 already resident in HBM.  W untimed warmup steps run eagerly; then K steps are
 captured into one hipGraph.  A second graph of the same K steps over other
-copies of the inputs is replayed first, untimed, so the GPU is busy and at its
-working clock when the timed graph starts; the timed graph is replayed between
+copies of the inputs is replayed first, untimed (as many times as take at
+least WARM_MS = 200 ms and move 2x the MALL), so the GPU is busy and at its
+sustained clock when the timed graph starts; the timed graph is replayed between
 two hipEvents on the stream the kernels run on, with torch.cuda.synchronize()
 before the untimed replay and after the stop event.  The timed steps read
 input copies that no launch has touched for at least 2x the 256 MiB MALL of
@@ -36,6 +37,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -53,6 +55,7 @@ CALIBRATION_KEY = {"fp16": "fp16_mma", "bf16": "bf16_mma", "fp8": "fp8_e4m3fn_mm
 
 MiB = 1024 * 1024
 MALL_BYTES = 256 * MiB
+WARM_MS = 200.0  # untimed back-to-back work before every timed replay (clock at its sustained level)
 
 
 # ----------------------------------------------------------------------------- workloads
@@ -445,11 +448,21 @@ def time_steps(w, timed, warm, steps: int, warmup: int) -> dict:
     g_warm, keep_w = _capture(w, warm, steps)
     g_timed, keep_t = _capture(w, timed, steps)
     g_timed.replay()  # uploads the timed graph; its sets are then evicted by the warm replays below
-    traffic = (_footprint(timed[0]) + w.get("out_bytes", 0)) * steps
-    warm_replays = max(1, -(-2 * MALL_BYTES // max(traffic, 1)))
     stream = torch.cuda.current_stream()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # One warm replay, timed, sizes the warm phase: at least 2x the MALL of
+    # traffic (the eviction above) and at least WARM_MS of back-to-back work, so
+    # the timed replay runs at the clock the GPU holds under sustained load
+    # whatever K is (a 20-step replay of a 0.3 ms kernel alone is 6 ms).
+    w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    w0.record(stream)
+    g_warm.replay()
+    w1.record(stream)
+    torch.cuda.synchronize()
+    per_replay = max(w0.elapsed_time(w1), 1e-3)
+    traffic = (_footprint(timed[0]) + w.get("out_bytes", 0)) * steps
+    warm_replays = max(1, -(-2 * MALL_BYTES // max(traffic, 1)), math.ceil(WARM_MS / per_replay))
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for _ in range(warm_replays):
         g_warm.replay()
     start.record(stream)
@@ -458,7 +471,8 @@ def time_steps(w, timed, warm, steps: int, warmup: int) -> dict:
     torch.cuda.synchronize()
     ms = start.elapsed_time(stop) / steps
     del keep_w, keep_t, g_warm, g_timed
-    return {"ms": ms, "untimed_replays_before": warm_replays, "timed_sets": len(timed), "warm_sets": len(warm)}
+    return {"ms": ms, "untimed_replays_before": warm_replays, "warm_ms": round(warm_replays * per_replay, 1),
+            "timed_sets": len(timed), "warm_sets": len(warm)}
 
 
 def measured_traffic(kernel: str):
@@ -651,9 +665,11 @@ def main(argv=None) -> int:
         "data": "synthetic (seeded CPU generator, resident in HBM)",
         "config": {**w["config"], "input_sets": main_res["timing"]["timed_sets"]},
         "timing": {"untimed_replays_before": main_res["timing"]["untimed_replays_before"],
+                   "warm_ms": main_res["timing"]["warm_ms"],
                    "warm_sets": main_res["timing"]["warm_sets"],
                    "region": "K steps in one hipGraph replay between hipEvents, after untimed replays of the "
-                             "same K steps on other input copies (no host sync between them)"},
+                             "same K steps on other input copies (at least 200 ms of them, no host sync "
+                             "between them and the timed replay)"},
         "roofline": main_res["roofline"],
         "cpu_baseline": main_res.get("cpu_baseline"),
     }
