@@ -28,7 +28,7 @@ def _check_rows(rows, min_kernel_ms=0.0):
         assert st["mean"] >= min_kernel_ms
         assert r["hip_ms"] == st["mean"]
         print(f"[timer] {r['params']} {r['dtype']}: kernel {st['mean'] * 1e3:.2f} us, "
-              f"event bracket {st['event_mean'] * 1e3:.2f} us, samples "
+              f"event bracket {st['event_mean'] * 1e3:.2f} us, profiled runs {st['timestamp_attempts']}, samples "
               f"{[round(v * 1e3, 2) for v in st['samples']]}", flush=True)
         assert r["torch_ms"] > 0 and r["torch_stats"]["mode"] in ("graph", "eager")
 

@@ -23,6 +23,8 @@ Two times come out of every sample:
     the L2's dirty lines visible to the host.  For a microsecond kernel that
     fixed cost is larger than the kernel, so it is reported, not used as the
     result.
+A profiled run whose records miss a kernel (the tracer reads its buffers
+asynchronously) is run again, up to TIMESTAMP_ATTEMPTS times in all.
 Without the activity records (profiler unavailable), or with an external
 rocprofiler tool attached to the process (rocprofv3 sets ROCP_TOOL_LIBRARIES;
 torch's activity records are then not trustworthy), ``mean`` falls back to the
@@ -44,6 +46,8 @@ DEFAULT_REPEAT = 3
 
 #: name fragment of the flush kernel (tb_l2_flush), told apart from run()'s kernels
 FLUSH_KERNEL = "fill_kernel"
+#: profiled runs tried before the events alone time a call
+TIMESTAMP_ATTEMPTS = 3
 
 _flush_buf: torch.Tensor | None = None
 
@@ -184,13 +188,19 @@ def report_benchmark(f: Callable[..., Any], tuple_of_args: tuple, kwargs: dict |
         torch.cuda.synchronize()
 
     kernel_ms = None
+    attempts = 0
     if kernel_timestamps and not external_profiler_attached():
+        # The activity records of a profiled run now and then miss a kernel
+        # (the tracer's buffers are read asynchronously); such a run is timed
+        # again, up to TIMESTAMP_ATTEMPTS times, before the events alone are used.
         try:
             from torch.profiler import ProfilerActivity, profile
 
-            with profile(activities=[ProfilerActivity.CUDA]) as prof:
-                sample_all()
-            kernel_ms = kernel_times_per_sample(_device_kernels(prof), n, flush_l2)
+            while kernel_ms is None and attempts < TIMESTAMP_ATTEMPTS:
+                attempts += 1
+                with profile(activities=[ProfilerActivity.CUDA]) as prof:
+                    sample_all()
+                kernel_ms = kernel_times_per_sample(_device_kernels(prof), n, flush_l2)
         except Exception:  # no activity records here: time with the events alone
             torch.cuda.synchronize()
             kernel_ms = None
@@ -203,4 +213,5 @@ def report_benchmark(f: Callable[..., Any], tuple_of_args: tuple, kwargs: dict |
             "max": max(samples), "samples": samples,
             "time_source": ("kernel timestamps" if kernel_ms is not None else
                             "hipEvents (rocprofiler tool attached)" if external_profiler_attached() else "hipEvents"),
+            "timestamp_attempts": attempts,
             "event_mean": sum(events) / n, "event_samples": events, "mode": mode, "flush_mb": flush_mb}
