@@ -141,6 +141,27 @@ def test_gating_filter_paths(gpu, E, k):
     np.testing.assert_allclose(w.cpu().numpy(), rw, atol=1e-5, rtol=1e-5, equal_nan=True)
 
 
+@pytest.mark.parametrize("E", [64, 128, 256])
+def test_gating_filter_ragged_row_counts(gpu, E):
+    """Row counts that leave part of the last block past M (whose lanes read
+    zeros and must write nothing): every row equals the oracle, and the rows
+    of a larger output buffer past M keep their contents."""
+    from tilebench_amd import runtime as rt
+
+    for M in (1, 15, 17, 33, 1009):
+        _say("gating filter ragged", E, M)
+        logits, M, E, k = T.generate_moe_topk_gating_inputs(M, E, 8, seed=M * E, device="cpu")
+        x = logits.to(gpu)
+        w = torch.full((M + 16, k), 7.0, device=gpu)
+        i = torch.full((M + 16, k), -7, dtype=torch.int32, device=gpu)
+        rt.call("tb_moe_topk_gating", x.data_ptr(), w.data_ptr(), i.data_ptr(), M, E, k, 0, rt.stream_handle())
+        torch.cuda.synchronize()
+        rw, ri = oracle.moe_topk_gating(logits.numpy(), k)
+        np.testing.assert_array_equal(i[:M].cpu().numpy(), ri)
+        np.testing.assert_allclose(w[:M].cpu().numpy(), rw, atol=1e-5, rtol=1e-5)
+        assert bool((w[M:] == 7.0).all()) and bool((i[M:] == -7).all())
+
+
 @pytest.mark.parametrize("E", [64, 256])
 @pytest.mark.parametrize("dt", ["fp16", "bf16"])
 def test_gating_filter_half_dtypes(gpu, E, dt):

@@ -7,16 +7,20 @@
 // shapes).  A row is owned by 16 lanes; each lane loads V logits
 // with 16-byte loads (8-byte when V·size < 16) laid out so that one load
 // instruction of the row's 16 lanes covers 256 contiguous bytes.  Per lane:
-//   1. the lane maximum m_q (signed-int order of the float bits, two VALU ops
-//      per element for the key, max3/min3 folds);
+//   1. the lane maximum m_q (a med3 chain on the fp32 values) and a flag
+//      that is NaN exactly when an element is inf or NaN (a sum of x * 0);
 //   2. T = the k-th largest of the 16 lane maxima (a bitonic network across
-//      the row's lanes).  The k lanes with the largest maxima hold k distinct
-//      elements >= T, so the row's k-th largest element is >= T, and every
-//      element the top-k can select is >= T;
+//      the row's lanes on their signed-int keys, each compare-exchange one
+//      max and one min with the partner read by DPP, and a select).  The k
+//      lanes with the largest maxima hold k distinct elements >= T, so the
+//      row's k-th largest element is >= T, and every element the top-k can
+//      select is >= T;
 //   3. the lane's candidates, elements >= T (float compare: -0 == +0), as a
-//      bit mask built with one compare and one add-with-carry per element;
+//      bit mask;
 //   4. the row's candidates are compacted (prefix sum of the lane counts) into
-//      an LDS list of exact (key, 1023 - index) pairs; with at most 16 of
+//      an LDS list of exact (key, 1023 - index) pairs (with V >= 8 by a loop
+//      over the mask's set bits, each value read back from an LDS copy of the
+//      lane's elements; with V = 4 by one masked write per element); with at most 16 of
 //      them, lane i takes candidate i and a bitonic network over the 16 lanes
 //      sorts them: lane t ends with the t-th selection.  With 17 to 32, lane i
 //      also takes candidate i + 16, both lists are sorted and merged (lane t
@@ -457,156 +461,311 @@ __device__ __forceinline__ uint64_t sort16_desc(uint64_t v, int p) {
   return cx_u64<0, 1>(v, p);
 }
 
-template <int DT, int V, int KMAX>
+// Partner value for a compare-exchange whose move the compiler folds into the
+// min / max that use it (v_max_i32_dpp): bound_ctrl with a zero old value.
+// Every pattern used here is a permutation of the 16-lane row, so no lane
+// reads outside it.
+template <int CTRL>
+__device__ __forceinline__ int32_t dpp_i32(int32_t v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+// Compare-exchange of one sorting stage: the lane keeps the larger value
+// unless (p & BIT), CTRL naming the partner (p ^ 1, p ^ 3, p ^ 7, p ^ 15 or
+// p ^ 2).
+template <int CTRL, int BIT>
+__device__ __forceinline__ int32_t cxf_i32(int32_t v, int p) {
+  const int32_t hi = max(v, dpp_i32<CTRL>(v)), lo = min(v, dpp_i32<CTRL>(v));
+  return (p & BIT) ? lo : hi;
+}
+// The distance-4 stage (partner p ^ 4, BIT = 4): lanes with bit 2 set keep
+// the minimum with lane p - 4 (row_ror:4), the others the maximum with lane
+// p + 4 (row_ror:12).
+__device__ __forceinline__ int32_t cxf4_i32(int32_t v, int p) {
+  const int32_t lo = min(v, dpp_i32<0x124>(v)), hi = max(v, dpp_i32<0x12C>(v));
+  return (p & 4) ? lo : hi;
+}
+// sort16_desc on G independent values per lane (rows of a lane group), stage
+// by stage, so the rows' dependent chains interleave.
+template <int G>
+__device__ __forceinline__ void sort16_desc_g(int32_t (&v)[G], int p) {
+#define TB_STAGE(expr)            \
+  _Pragma("unroll") for (int g = 0; g < G; ++g) { \
+    const int32_t x = v[g];       \
+    v[g] = expr;                  \
+  }
+  TB_STAGE((cxf_i32<0xB1, 1>(x, p)))
+  TB_STAGE((cxf_i32<0x1B, 2>(x, p)))
+  TB_STAGE((cxf_i32<0xB1, 1>(x, p)))
+  TB_STAGE((cxf_i32<0x141, 4>(x, p)))
+  TB_STAGE((cxf_i32<0x4E, 2>(x, p)))
+  TB_STAGE((cxf_i32<0xB1, 1>(x, p)))
+  TB_STAGE((cxf_i32<0x140, 8>(x, p)))
+  TB_STAGE((cxf4_i32(x, p)))
+  TB_STAGE((cxf_i32<0x4E, 2>(x, p)))
+  TB_STAGE((cxf_i32<0xB1, 1>(x, p)))
+#undef TB_STAGE
+}
+
+// Lane n (0 <= n < 16, a run-time value) of the caller's 16-lane row, through
+// the LDS crossbar (ds_bpermute).
+__device__ __forceinline__ int32_t row_lane(int32_t v, int n) {
+  const int src = (int)(threadIdx.x & 48u) + n;
+  return __builtin_amdgcn_ds_bpermute(src << 2, v);
+}
+
+// Geometry of the filter kernel for E = 16·V elements of ESZ bytes.
+template <int DT, int V>
+struct FilterShape {
+  static constexpr int LPR = 16;                          // lanes per row
+  static constexpr int E = LPR * V;
+  static constexpr int ESZ = DT == 0 ? 4 : 2;
+  static constexpr int ROWB = E * ESZ;                    // bytes per row
+  static constexpr int CB = V * ESZ < 16 ? V * ESZ : 16;  // bytes per load
+  static constexpr int NC = V * ESZ / CB;                 // loads per lane
+  static constexpr int EPC = CB / ESZ;                    // elements per load
+  static constexpr int CW = CB / 4;                       // words per load
+  static constexpr int ROWS = kBlock / LPR;               // rows of a row group
+  static constexpr bool STAGED = V >= 8;                  // candidates gathered from an LDS copy
+  static constexpr int SSTRIDE = V + 4;                   // words per lane of that copy (16-byte multiple)
+  static_assert(CB == 8 || CB == 16, "filter_kernel: 8- or 16-byte loads");
+};
+
+// A block owns G row groups of ROWS consecutive rows: group g holds rows
+// G*ROWS*blockIdx.x + g*ROWS .. +ROWS-1, one row per 16 lanes, so each lane
+// group works on G rows at once, every step issued for all of them together
+// (their dependent chains interleave, and the grid has G times fewer
+// wavefronts to dispatch).  Every load goes through a buffer resource over the
+// block's rows: rows past M read zeros, move no data and are not stored.
+template <int DT, int V, int KMAX, int G>
 __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__ logits, void* __restrict__ weights,
                                                         int32_t* __restrict__ indices, int64_t M, int k) {
-  constexpr int LPR = 16;
-  constexpr int E = LPR * V;
-  constexpr int ESZ = DT == 0 ? 4 : 2;
-  constexpr int ROWB = E * ESZ;                       // bytes per row
-  constexpr int CB = V * ESZ < 16 ? V * ESZ : 16;     // bytes per load
-  constexpr int NC = V * ESZ / CB;                    // loads per lane
-  constexpr int EPC = CB / ESZ;                       // elements per load
-  constexpr int CW = CB / 4;                          // words per load
-  constexpr int ROWS = kBlock / LPR;
-  static_assert(CB == 8 || CB == 16, "filter_kernel: 8- or 16-byte loads");
+  using S = FilterShape<DT, V>;
+  constexpr int LPR = S::LPR, ESZ = S::ESZ, ROWB = S::ROWB, CB = S::CB, NC = S::NC, EPC = S::EPC, CW = S::CW,
+                ROWS = S::ROWS;
+  constexpr int NT = 2;  // nontemporal: every logit is read once
+  constexpr int DUMMY = 2 * LPR;  // list entry taking the writes of lanes with nothing to write
 
-  __shared__ uint64_t cand[ROWS][2 * LPR];
+  __shared__ uint64_t cand[G][ROWS][2 * LPR + 1];
+  __shared__ uint32_t staged[S::STAGED ? G * kBlock * S::SSTRIDE : 1];
 
   const int slot = threadIdx.x / LPR;
   const int q = threadIdx.x % LPR;
-  const int64_t r = (int64_t)blockIdx.x * ROWS + slot;
-  if (r >= M) return;  // whole rows leave together; every exchange below stays inside a row
+  const int64_t r0 = (int64_t)blockIdx.x * (ROWS * G);
+  const int64_t here = M - r0 < (int64_t)(ROWS * G) ? M - r0 : (int64_t)(ROWS * G);  // rows of this block
+  const buf_rsrc_t rl = buf_rsrc(reinterpret_cast<const char*>(logits) + r0 * ROWB, (uint32_t)(here * ROWB));
 
   // Load c of lane q covers row elements c*16*EPC + q*EPC + (0 .. EPC-1), so
-  // one load instruction of the row's lanes reads 16*CB contiguous bytes.
-  uint32_t w[NC * CW];
-  {
-    const char* rowp = reinterpret_cast<const char*>(logits) + r * ROWB;
+  // one load instruction of a row's lanes reads 16*CB contiguous bytes.
+  uint32_t w[G][NC * CW];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int row = g * ROWS + slot;
+    const uint32_t base = row < here ? (uint32_t)(row * ROWB + q * CB) : BUF_OOB;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const int off = c * LPR * CB + q * CB;
       if constexpr (CB == 16) {
-        const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rowp + off));
+        const u32x4 x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rl, base, c * LPR * CB, NT));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) w[c * 4 + i] = x[i];
+        for (int i = 0; i < 4; ++i) w[g][c * 4 + i] = x[i];
       } else {
-        const u32x2 x = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(rowp + off));
+        const u32x2 x = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rl, base, c * LPR * CB, NT));
 #pragma unroll
-        for (int i = 0; i < 2; ++i) w[c * 2 + i] = x[i];
+        for (int i = 0; i < 2; ++i) w[g][c * 2 + i] = x[i];
       }
     }
   }
-  uint32_t f[V];  // fp32 bits of the lane's elements, j = c*EPC + i
+  bool live[G];
 #pragma unroll
-  for (int j = 0; j < V; ++j) f[j] = f32_bits<DT>(w[j * ESZ / 4], j & 1);
+  for (int g = 0; g < G; ++g) live[g] = g * ROWS + slot < here;
 
-  // 1. lane maximum and minimum in flip-key order
-  int32_t kmax = flip_key(f[0]), kmin = kmax;
+  // fp32 values of the lane's elements, j = c*EPC + i; the lane maximum
+  // (med3 with +inf is the larger of two finite values) and a flag that is NaN
+  // exactly when an element is not finite (x * 0 is NaN for inf and NaN).
+  float f[G][V];
+  int32_t kmax[G];
+  bool finite = true;
 #pragma unroll
-  for (int j = 1; j < V; ++j) {
-    const int32_t kj = flip_key(f[j]);
-    kmax = kmax > kj ? kmax : kj;
-    kmin = kmin < kj ? kmin : kj;
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int j = 0; j < V; ++j) f[g][j] = __builtin_bit_cast(float, f32_bits<DT>(w[g][j * ESZ / 4], j & 1));
+    float mx = f[g][0], nf0 = 0.f, nf1 = 0.f;
+#pragma unroll
+    for (int j = 1; j < V; ++j) mx = __builtin_amdgcn_fmed3f(mx, f[g][j], __builtin_inff());
+#pragma unroll
+    for (int j = 0; j < V; j += 2) {
+      nf0 = __builtin_fmaf(f[g][j], 0.f, nf0);
+      if (j + 1 < V) nf1 = __builtin_fmaf(f[g][j + 1], 0.f, nf1);
+    }
+    finite = finite && (nf0 + nf1 == 0.f);
+    kmax[g] = flip_key(__builtin_bit_cast(uint32_t, mx));
   }
-  // +inf / +NaN keys are >= flip(0x7F800000); -inf / -NaN keys are <= flip(0xFF800000).
-  const bool finite = kmax < 0x7F800000 && kmin > (int32_t)0x807FFFFFu;
-
-  // 2. T = the k-th largest lane maximum (flip order refines float order, so
-  // the k lanes above it hold k elements that are >= T as floats)
-  const int32_t tkey = (int32_t)row_bcast_lt8((uint32_t)sort16_desc(kmax, q), k - 1);  // k <= KMAX = 8
-  const float T = __builtin_bit_cast(float, (uint32_t)flip_key((uint32_t)tkey));
-
-  // 3. candidate mask, bit j for element j
-  uint32_t mask = 0;
+  if constexpr (S::STAGED) {
+    // the lane's elements, for the candidate gather below
 #pragma unroll
-  for (int j = V - 1; j >= 0; --j) mask = mask + mask + (uint32_t)(__builtin_bit_cast(float, f[j]) >= T);
-  const int cnt = __builtin_popcount(mask);
-
-  // inclusive prefix of the counts across the row's 16 lanes
-  int incl = cnt;
-  incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xF, 0xF, true);  // row_shr:1
-  incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, true);  // row_shr:2
-  incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, true);  // row_shr:4
-  incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, true);  // row_shr:8
-  const int total = (int)row_bcast<LPR - 1>((uint32_t)incl);
-
-  if (__builtin_amdgcn_ballot_w64(!(finite && total <= 2 * LPR)) == 0) {
-    // 4. compact the row's candidates into cand[slot], each as the exact
-    // (key, 1023 - index) pair, so a lane reads its candidate in one step
-    // (candidate j of the lane goes to its slot among the row's: the lane's
-    // base plus the candidates before it in the lane, a popcount, so the
-    // writes do not wait on one another)
-    const int base = incl - cnt;
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int j = 0; j < V; ++j)
-      if ((mask >> j) & 1u) {
-        const int idx = (j / EPC) * (LPR * EPC) + q * EPC + (j % EPC);
-        cand[slot][base + __builtin_popcount(mask & ((1u << j) - 1u))] =
-            ((uint64_t)key_of_bits(f[j]) << 32) | (uint32_t)(1023 - idx);
+      for (int j = 0; j < V; j += 4)
+        *reinterpret_cast<u32x4*>(&staged[(g * kBlock + threadIdx.x) * S::SSTRIDE + j]) =
+            __builtin_bit_cast(u32x4, f32x4{f[g][j], f[g][j + 1], f[g][j + 2], f[g][j + 3]});
+  }
+
+  // T = the k-th largest lane maximum of the row (k <= KMAX = 8): the k lanes
+  // above it hold k elements >= T, so every element the top-k can select is >= T.
+  sort16_desc_g<G>(kmax, q);
+  float T[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) T[g] = __builtin_bit_cast(float, (uint32_t)flip_key((uint32_t)row_lane(kmax[g], k - 1)));
+
+  // candidate mask (bit j for element j), counts and their inclusive prefix
+  // across the row's 16 lanes
+  uint32_t mask[G];
+  int cnt[G], incl[G], total[G];
+  bool fast = finite;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = V - 1; j >= 0; --j) m = m + m + (uint32_t)(f[g][j] >= T[g]);
+    mask[g] = live[g] ? m : 0u;  // rows past M (zeros) have no candidates: nothing is written for them
+    cnt[g] = __builtin_popcount(m);
+    int x = cnt[g];
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);  // row_shr:8
+    incl[g] = x;
+    total[g] = (int)row_bcast<LPR - 1>((uint32_t)x);
+    fast = fast && (!live[g] || total[g] <= 2 * LPR);
+  }
+
+  if (__builtin_amdgcn_ballot_w64(!fast) == 0) {
+    // Each candidate goes to the row's LDS list as the exact (key, 1023 - index)
+    // pair, at its slot among the row's: the lane's base plus its candidates
+    // before it.
+    if constexpr (S::STAGED) {
+      // a loop over the set bits of the masks (about one candidate per lane),
+      // each candidate's value read back from the lane's LDS copy; a lane
+      // with nothing left in a row writes to the row's spare entry
+      uint32_t m[G];
+      int dst[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        m[g] = mask[g];
+        dst[g] = incl[g] - cnt[g];
       }
-    // The list is read by other lanes of this wavefront only (each wavefront
-    // owns its rows' LDS), so a wavefront-scope fence orders the accesses.
+      uint32_t any = 0;
+#pragma unroll
+      for (int g = 0; g < G; ++g) any |= m[g];
+      while (any != 0) {
+        any = 0;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const bool has = m[g] != 0;
+          const int j = has ? __builtin_ctz(m[g]) : 0;
+          m[g] &= m[g] - 1u;
+          const uint32_t fj = staged[(g * kBlock + threadIdx.x) * S::SSTRIDE + j];
+          const int idx = (j / EPC) * (LPR * EPC) + q * EPC + (j % EPC);
+          cand[g][slot][has ? dst[g] : DUMMY] = ((uint64_t)key_of_bits(fj) << 32) | (uint32_t)(1023 - idx);
+          dst[g] += has;
+          any |= m[g];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const int base = incl[g] - cnt[g];
+#pragma unroll
+        for (int j = 0; j < V; ++j)
+          if ((mask[g] >> j) & 1u) {
+            const int idx = (j / EPC) * (LPR * EPC) + q * EPC + (j % EPC);
+            cand[g][slot][base + __builtin_popcount(mask[g] & ((1u << j) - 1u))] =
+                ((uint64_t)key_of_bits(__builtin_bit_cast(uint32_t, f[g][j])) << 32) | (uint32_t)(1023 - idx);
+          }
+      }
+    }
+    // The lists are read by other lanes of this wavefront only (each
+    // wavefront owns its rows' LDS), so a wavefront-scope fence orders the
+    // accesses.
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // lane q takes candidate q; 0 marks no candidate
-    uint64_t v = q < total ? cand[slot][q] : 0;
-    if (__builtin_amdgcn_ballot_w64(total > LPR) == 0) {
-      v = sort16_desc(v, q);
+    uint64_t v[G];
+    bool big = false;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      v[g] = q < total[g] ? cand[g][slot][q] : 0;
+      big = big || (live[g] && total[g] > LPR);
+    }
+    if (__builtin_amdgcn_ballot_w64(big) == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) v[g] = sort16_desc(v[g], q);
     } else {
       // a row of this wavefront has 17..32 candidates: lane q also takes
       // candidate q + 16, both lists are sorted, and lane t keeps the larger
       // of v[t] and v1[15 - t]; those 16 are the top 16 of the union as a
       // bitonic sequence, which the half-cleaners at distances 8, 4, 2, 1 sort
-      uint64_t v1 = q + LPR < total ? cand[slot][q + LPR] : 0;
-      v = sort16_desc(v, q);
-      v1 = sort16_desc(v1, q);
-      const u32x2 b = __builtin_bit_cast(u32x2, v1);
-      const uint64_t m = __builtin_bit_cast(uint64_t, u32x2{partner16<5>(b.x), partner16<5>(b.y)});
-      v = v > m ? v : m;
-      v = cx_u64<6, 8>(v, q);
-      v = cx_u64<2, 4>(v, q);
-      v = cx_u64<1, 2>(v, q);
-      v = cx_u64<0, 1>(v, q);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        uint64_t v1 = q + LPR < total[g] ? cand[g][slot][q + LPR] : 0;
+        v[g] = sort16_desc(v[g], q);
+        v1 = sort16_desc(v1, q);
+        const u32x2 b = __builtin_bit_cast(u32x2, v1);
+        const uint64_t mm = __builtin_bit_cast(uint64_t, u32x2{partner16<5>(b.x), partner16<5>(b.y)});
+        v[g] = v[g] > mm ? v[g] : mm;
+        v[g] = cx_u64<6, 8>(v[g], q);
+        v[g] = cx_u64<2, 4>(v[g], q);
+        v[g] = cx_u64<1, 2>(v[g], q);
+        v[g] = cx_u64<0, 1>(v[g], q);
+      }
     }
 
-    // lane t < k holds selection t
-    const float val = float_of_key((uint32_t)(v >> 32));
-    const float v0 = row_bcast_f<0>(val);
-    const float et = q < k ? expf(val - v0) : 0.f;
-    float e[KMAX];
-    bcast_all(et, e, std::make_integer_sequence<int, KMAX>{});
-    const float sum = np_sum<KMAX>(e, k);
-    if (q < k) {
-      store_weight<DT>(weights, r * k + q, et / sum);
-      indices[r * k + q] = 1023 - (int)(uint32_t)v;
+    // lane t < k holds selection t of its row
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float val = float_of_key((uint32_t)(v[g] >> 32));
+      const float v0 = row_bcast_f<0>(val);
+      const float et = q < k ? expf(val - v0) : 0.f;
+      float e[KMAX];
+      bcast_all(et, e, std::make_integer_sequence<int, KMAX>{});
+      const float sum = np_sum<KMAX>(e, k);
+      const int64_t r = r0 + g * ROWS + slot;
+      if (live[g] && q < k) {
+        store_weight<DT>(weights, r * k + q, et / sum);
+        indices[r * k + q] = 1023 - (int)(uint32_t)v[g];
+      }
     }
   } else {
-    // exact path: lane q takes elements q*V .. q*V+V-1.  With one load per
-    // lane it already holds them; otherwise it reads them again (this path is
-    // rare) rather than staging every row in LDS.
-    uint32_t u[V];
-    if constexpr (NC == 1) {
+    // exact path for every row of the wavefront: lane q takes elements
+    // q*V .. q*V+V-1.  With one load per lane it already holds them;
+    // otherwise it reads them again (this path is rare).  Unrolled: a
+    // run-time row index into f would move f out of registers.
 #pragma unroll
-      for (int j = 0; j < V; ++j) u[j] = key_of_bits(f[j]);
-    } else {
-      const uint32_t* rw = reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(logits) + r * ROWB) +
-                           q * V * ESZ / 4;
-      uint32_t x[V * ESZ / 4];
+    for (int g = 0; g < G; ++g) {
+      if (!live[g]) continue;
+      const int64_t r = r0 + g * ROWS + slot;
+      uint32_t u[V];
+      if constexpr (NC == 1) {
 #pragma unroll
-      for (int c = 0; c < V * ESZ / 16; ++c) {
-        const u32x4 t = *reinterpret_cast<const u32x4*>(rw + 4 * c);
+        for (int j = 0; j < V; ++j) u[j] = key_of_bits(__builtin_bit_cast(uint32_t, f[g][j]));
+      } else {
+        const uint32_t* rw = reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(logits) + r * ROWB) +
+                             q * V * ESZ / 4;
+        uint32_t x[V * ESZ / 4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) x[4 * c + i] = t[i];
+        for (int c = 0; c < V * ESZ / 16; ++c) {
+          const u32x4 t = *reinterpret_cast<const u32x4*>(rw + 4 * c);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[4 * c + i] = t[i];
+        }
+#pragma unroll
+        for (int j = 0; j < V; ++j) u[j] = key_of_bits(f32_bits<DT>(x[j * ESZ / 4], j & 1));
       }
-#pragma unroll
-      for (int j = 0; j < V; ++j) u[j] = key_of_bits(f32_bits<DT>(x[j * ESZ / 4], j & 1));
+      double sel[KMAX];
+      exact_select<V, LPR, KMAX>(u, q, sel);
+      write_selected<DT, LPR, KMAX>(sel, r, q, k, weights, indices);
     }
-    double sel[KMAX];
-    exact_select<V, LPR, KMAX>(u, q, sel);
-    write_selected<DT, LPR, KMAX>(sel, r, q, k, weights, indices);
   }
 }
 
@@ -623,10 +782,15 @@ static tb_status launch(const void* logits, void* weights, int32_t* indices, int
 template <int DT, int V, int KMAX>
 static tb_status launch_filter(const void* logits, void* weights, int32_t* indices, int64_t M, int k,
                                hipStream_t stream) {
+  // One row per lane group: two or four rows per lane group (half or a
+  // quarter of the wavefronts, each row's steps interleaved with the others')
+  // measured 20-60 % slower, the wavefronts hiding each other's latencies
+  // better than a wavefront's rows do.
+  constexpr int G = 1;
   constexpr int ROWS = kBlock / 16;
-  const int64_t blocks = (M + ROWS - 1) / ROWS;
-  hipLaunchKernelGGL((filter_kernel<DT, V, KMAX>), dim3((unsigned)blocks), dim3(kBlock), 0, stream, logits, weights,
-                     indices, M, k);
+  const int64_t blocks = (M + ROWS * G - 1) / (ROWS * G);
+  hipLaunchKernelGGL((filter_kernel<DT, V, KMAX, G>), dim3((unsigned)blocks), dim3(kBlock), 0, stream, logits,
+                     weights, indices, M, k);
   return launch_status("tb_moe_topk_gating");
 }
 
