@@ -215,6 +215,31 @@ def test_fp8_quotient_scheme_exhaustive_c():
                 os.remove(f)
 
 
+def test_gating_key_maps_exhaustive_c():
+    """The gating filter kernel's NaN-free key map equals the general one on
+    every finite fp32 pattern, and key order is float order with -0 == +0;
+    the same program with the map's sign correction dropped must fail."""
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    src = os.path.join(ROOT, "tests", "native", "gating_key_check.c")
+    out = os.path.join(ROOT, "tests", "native", "_gating_key_check")
+    bad = out + "_planted"
+    flags = ["-O2", "-fopenmp"]
+    subprocess.run([gcc, *flags, src, "-o", out], check=True)
+    subprocess.run([gcc, *flags, "-DPLANT_DROPPED_SUBTRACT", src, "-o", bad], check=True)
+    try:
+        good = subprocess.run([out], capture_output=True, text=True, timeout=600)
+        assert good.returncode == 0, good.stdout
+        assert "mismatches=0 order_errors=0" in good.stdout
+        planted = subprocess.run([bad], capture_output=True, text=True, timeout=600)
+        assert planted.returncode != 0 and "mismatches=0" not in planted.stdout
+    finally:
+        for f in (out, bad):
+            if os.path.exists(f):
+                os.remove(f)
+
+
 # ----------------------------------------------------------------------------- GEMMs
 
 

@@ -68,6 +68,14 @@ __device__ __forceinline__ uint32_t key_of_bits(uint32_t b) {
   return mag > 0x7F800000u ? 0xFFFFFFFFu : key;
 }
 
+// key_of_bits for a finite value (no NaN check): with s the sign mask,
+// b ^ (s & 0x7FFFFFFF) ^ 0x80000000 minus s, i.e. 0x80000000 + |x| bits for
+// x >= 0 and 0x80000000 - |x| bits for x < 0 (one bitop3 and one subtract).
+__device__ __forceinline__ uint32_t key_of_finite(uint32_t b) {
+  const uint32_t sm = (uint32_t)((int32_t)b >> 31);
+  return (b ^ (sm & 0x7FFFFFFFu) ^ 0x80000000u) - sm;
+}
+
 __device__ __forceinline__ float float_of_key(uint32_t u) {
   const uint32_t b = u >= 0x80000000u ? u - 0x80000000u : 0x80000000u | (0x80000000u - u);
   return __builtin_bit_cast(float, b);
@@ -78,6 +86,21 @@ __device__ __forceinline__ float float_of_key(uint32_t u) {
 // map is its own inverse.
 __device__ __forceinline__ int32_t flip_key(uint32_t b) {
   return (int32_t)(b ^ ((uint32_t)((int32_t)b >> 31) & 0x7FFFFFFFu));
+}
+
+// e^x for finite x <= 0: expf's own sequence (x log2 e as a rounded product
+// plus its error from an fma and the low part of log2 e, 2^fraction by
+// v_exp_f32, scaled by 2^round) without its overflow and underflow tests,
+// which only matter outside that range (below about -104 it returns a
+// denormal or zero where expf returns zero).
+__device__ __forceinline__ float exp_nonpos(float x) {
+#pragma clang fp contract(off)
+  const float hi = __builtin_bit_cast(float, 0x3FB8AA3Bu);  // log2(e) rounded to fp32
+  const float lo = __builtin_bit_cast(float, 0x32A5705Fu);  // log2(e) - hi
+  const float ph = x * hi;
+  const float pl = __builtin_fmaf(x, lo, __builtin_fmaf(x, hi, -ph));
+  const float r = __builtin_rintf(ph);
+  return __builtin_ldexpf(__builtin_amdgcn_exp2f((ph - r) + pl), (int)r);
 }
 
 // Round-to-nearest-even fp32 -> bf16 (NaN stays a quiet NaN).
@@ -154,6 +177,12 @@ __device__ __forceinline__ float np_sum(const float (&e)[N], int n) {
 }
 
 constexpr int kBlock = 256;
+#ifndef TB_FILTER_BLOCK
+#define TB_FILTER_BLOCK 64
+#endif
+// Threads per filter-kernel block: one wavefront (measured 1-4 % faster than
+// blocks of 128 or 256 threads).
+constexpr int kFilterBlock = TB_FILTER_BLOCK;
 
 // Exchange with the partner lane of butterfly step `step` inside a group of
 // LPR lanes.  Steps 0-3 (partners within 16 lanes) are DPP moves: quad swaps
@@ -524,7 +553,7 @@ struct FilterShape {
   static constexpr int NC = V * ESZ / CB;                 // loads per lane
   static constexpr int EPC = CB / ESZ;                    // elements per load
   static constexpr int CW = CB / 4;                       // words per load
-  static constexpr int ROWS = kBlock / LPR;               // rows of a row group
+  static constexpr int ROWS = kFilterBlock / LPR;         // rows of a row group
   static constexpr bool STAGED = V >= 8;                  // candidates gathered from an LDS copy
   static constexpr int SSTRIDE = V + 4;                   // words per lane of that copy (16-byte multiple)
   static_assert(CB == 8 || CB == 16, "filter_kernel: 8- or 16-byte loads");
@@ -536,9 +565,10 @@ struct FilterShape {
 // (their dependent chains interleave, and the grid has G times fewer
 // wavefronts to dispatch).  Every load goes through a buffer resource over the
 // block's rows: rows past M read zeros, move no data and are not stored.
-template <int DT, int V, int KMAX, int G>
-__global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__ logits, void* __restrict__ weights,
+template <int DT, int V, int KMAX, int G, bool KFIX>
+__global__ void __launch_bounds__(kFilterBlock) filter_kernel(const void* __restrict__ logits, void* __restrict__ weights,
                                                         int32_t* __restrict__ indices, int64_t M, int k) {
+  if constexpr (KFIX) k = KMAX;  // k == KMAX known at compile time (the BASELINE k = 8)
   using S = FilterShape<DT, V>;
   constexpr int LPR = S::LPR, ESZ = S::ESZ, ROWB = S::ROWB, CB = S::CB, NC = S::NC, EPC = S::EPC, CW = S::CW,
                 ROWS = S::ROWS;
@@ -546,7 +576,7 @@ __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__
   constexpr int DUMMY = 2 * LPR;  // list entry taking the writes of lanes with nothing to write
 
   __shared__ uint64_t cand[G][ROWS][2 * LPR + 1];
-  __shared__ uint32_t staged[S::STAGED ? G * kBlock * S::SSTRIDE : 1];
+  __shared__ uint32_t staged[S::STAGED ? G * kFilterBlock * S::SSTRIDE : 1];
 
   const int slot = threadIdx.x / LPR;
   const int q = threadIdx.x % LPR;
@@ -605,7 +635,7 @@ __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__
     for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int j = 0; j < V; j += 4)
-        *reinterpret_cast<u32x4*>(&staged[(g * kBlock + threadIdx.x) * S::SSTRIDE + j]) =
+        *reinterpret_cast<u32x4*>(&staged[(g * kFilterBlock + threadIdx.x) * S::SSTRIDE + j]) =
             __builtin_bit_cast(u32x4, f32x4{f[g][j], f[g][j + 1], f[g][j + 2], f[g][j + 3]});
   }
 
@@ -614,7 +644,10 @@ __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__
   sort16_desc_g<G>(kmax, q);
   float T[G];
 #pragma unroll
-  for (int g = 0; g < G; ++g) T[g] = __builtin_bit_cast(float, (uint32_t)flip_key((uint32_t)row_lane(kmax[g], k - 1)));
+  for (int g = 0; g < G; ++g) {
+    const int32_t tk = KFIX ? (int32_t)row_bcast<KMAX - 1>((uint32_t)kmax[g]) : row_lane(kmax[g], k - 1);
+    T[g] = __builtin_bit_cast(float, (uint32_t)flip_key((uint32_t)tk));
+  }
 
   // candidate mask (bit j for element j), counts and their inclusive prefix
   // across the row's 16 lanes
@@ -663,9 +696,9 @@ __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__
           const bool has = m[g] != 0;
           const int j = has ? __builtin_ctz(m[g]) : 0;
           m[g] &= m[g] - 1u;
-          const uint32_t fj = staged[(g * kBlock + threadIdx.x) * S::SSTRIDE + j];
+          const uint32_t fj = staged[(g * kFilterBlock + threadIdx.x) * S::SSTRIDE + j];
           const int idx = (j / EPC) * (LPR * EPC) + q * EPC + (j % EPC);
-          cand[g][slot][has ? dst[g] : DUMMY] = ((uint64_t)key_of_bits(fj) << 32) | (uint32_t)(1023 - idx);
+          cand[g][slot][has ? dst[g] : DUMMY] = ((uint64_t)key_of_finite(fj) << 32) | (uint32_t)(1023 - idx);
           dst[g] += has;
           any |= m[g];
         }
@@ -679,7 +712,7 @@ __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__
           if ((mask[g] >> j) & 1u) {
             const int idx = (j / EPC) * (LPR * EPC) + q * EPC + (j % EPC);
             cand[g][slot][base + __builtin_popcount(mask[g] & ((1u << j) - 1u))] =
-                ((uint64_t)key_of_bits(__builtin_bit_cast(uint32_t, f[g][j])) << 32) | (uint32_t)(1023 - idx);
+                ((uint64_t)key_of_finite(__builtin_bit_cast(uint32_t, f[g][j])) << 32) | (uint32_t)(1023 - idx);
           }
       }
     }
@@ -726,7 +759,7 @@ __global__ void __launch_bounds__(kBlock) filter_kernel(const void* __restrict__
     for (int g = 0; g < G; ++g) {
       const float val = float_of_key((uint32_t)(v[g] >> 32));
       const float v0 = row_bcast_f<0>(val);
-      const float et = q < k ? expf(val - v0) : 0.f;
+      const float et = q < k ? exp_nonpos(val - v0) : 0.f;  // val <= v0, the row maximum
       float e[KMAX];
       bcast_all(et, e, std::make_integer_sequence<int, KMAX>{});
       const float sum = np_sum<KMAX>(e, k);
@@ -787,10 +820,14 @@ static tb_status launch_filter(const void* logits, void* weights, int32_t* indic
   // measured 20-60 % slower, the wavefronts hiding each other's latencies
   // better than a wavefront's rows do.
   constexpr int G = 1;
-  constexpr int ROWS = kBlock / 16;
+  constexpr int ROWS = kFilterBlock / 16;
   const int64_t blocks = (M + ROWS * G - 1) / (ROWS * G);
-  hipLaunchKernelGGL((filter_kernel<DT, V, KMAX, G>), dim3((unsigned)blocks), dim3(kBlock), 0, stream, logits,
-                     weights, indices, M, k);
+  if (k == KMAX)
+    hipLaunchKernelGGL((filter_kernel<DT, V, KMAX, G, true>), dim3((unsigned)blocks), dim3(kFilterBlock), 0, stream,
+                       logits, weights, indices, M, k);
+  else
+    hipLaunchKernelGGL((filter_kernel<DT, V, KMAX, G, false>), dim3((unsigned)blocks), dim3(kFilterBlock), 0, stream,
+                       logits, weights, indices, M, k);
   return launch_status("tb_moe_topk_gating");
 }
 
