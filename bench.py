@@ -98,7 +98,7 @@ def _w_gating(E):
                     metric="MoE gating HBM throughput", unit="GB/s", dtype="fp32", bound="hbm", bytes=nbytes,
                     flops=None, out_bytes=M * k * 8,
                     inputs=lambda: T.generate_moe_topk_gating_inputs(M, E, k, seed=3, device="cuda"),
-                    step=lambda x: impl_hip.run(*x), kernel=f"tb::filter_kernel<0, {E // 16}, 8>", cpu=cpu)
+                    step=lambda x: impl_hip.run(*x), kernel=f"tb::filter_kernel<0, {E // 16}, 8, 1, true>", cpu=cpu)
     return make
 
 

@@ -47,7 +47,7 @@ CASES = [
     ("matmul_fp32_fp16_fp8", {"M": 1024, "N": 1024, "K": 1024, "dtype": "fp32"},
      [r"tb::ntg::split_rows", r"tb::ntg::split_transpose", r"tb::ntg::nt_gemm<2, 3, \d+, \d+, \d+, \d+>"]),
     ("fp8_act_quant", {"M": 256, "K": 4096, "dtype": "fp16"}, [r"tb::fp8_quant_rows<\d+>"]),
-    ("moe_topk_gating", {"M": 1024, "E": 64, "k": 8, "dtype": "fp32"}, [r"tb::filter_kernel<0, 4, 8>"]),
+    ("moe_topk_gating", {"M": 1024, "E": 64, "k": 8, "dtype": "fp32"}, [r"tb::filter_kernel<0, 4, 8, 1, true>"]),
     ("moe_topk_gating", {"M": 1024, "E": 128, "k": 2, "dtype": "fp16"}, [r"tb::gating_kernel<1, 16, 8, 2>"]),
 ]
 
