@@ -113,6 +113,34 @@ tb_status tb_w4a16_gemm(const uint16_t* A, const uint8_t* W, const uint16_t* sca
 tb_status tb_w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int64_t group, int64_t* bytes);
 
 /*
+ * Slab-contiguous copy of W for the decode below: Wr (K * N / 2 bytes, 16-byte
+ * aligned) holds slab s = columns 64 s .. 64 s + 63 as one contiguous run of
+ * K / 32 units of 1 KiB; unit u, lane l, word b (4 bytes at byte
+ * ((s * K / 32 + u) * 64 + l) * 16 + 4 b) holds the codes of column
+ * 64 s + 16 b + l % 16 at rows 32 u + 8 (l / 16) + i, i = 0..7, code i at bit
+ * (i % 2) * 16 + (i / 2) * 4.  Requires K % 32 == 0, N % 64 == 0.  Built once
+ * per weight tensor (the caller keeps it with the weights).  No counterpart in
+ * the reference, which has no W4A16 operator; it plays the part of the
+ * reference's cached column-major fp8 operand
+ * (matmul_fp32_fp16_fp8/impl_torch.py:7-18), a per-weight copy in the layout
+ * the kernel reads.
+ */
+tb_status tb_w4a16_repack_slabs(const uint8_t* W, uint8_t* Wr, int64_t K, int64_t N, hipStream_t stream);
+
+/*
+ * W4A16 GEMM for 1 <= M <= 16 from the slab copy: one block per 64-column slab
+ * streams its slab over all of K and reduces across its own wavefronts (no
+ * split-K, no workspace).  Same operands and result tolerance as
+ * tb_w4a16_gemm's decode (fp32 accumulation of the codes, scale and zero-point
+ * applied once per group; results reproducible bit for bit).  Requires
+ * N % 64 == 0, G in {64, 128}, K in {1024, 2048, 4096}, K % (16 G) == 0; A
+ * and Wr 16-byte aligned.  No counterpart in the reference (see
+ * tb_w4a16_repack_slabs).
+ */
+tb_status tb_w4a16_gemm_slabs(const uint16_t* A, const uint8_t* Wr, const uint16_t* scales, const uint8_t* zeros,
+                              uint16_t* Y, int64_t M, int64_t N, int64_t K, int64_t group, hipStream_t stream);
+
+/*
  * tb_w4a16_gemm without a workspace and without any allocation: for callers
  * that cannot allocate device memory (code under hipGraph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  No counterpart in the

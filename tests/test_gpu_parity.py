@@ -333,7 +333,7 @@ def test_w4a16_decode_repeat_calls_reuse_workspace(gpu):
     _say("w4a16_gemm decode repeat")
     A, p, s, z, G = T.generate_w4a16_gemm_inputs(16, 4096, 11008, 128, seed=5, device="cpu")
     args = (A.to(gpu), p.to(gpu), s.to(gpu), z.to(gpu), G)
-    outs = [impl_hip.run(*args) for _ in range(3)]
+    outs = [impl_hip.run(*args, slabs=False) for _ in range(3)]
     torch.cuda.synchronize()
     first = outs[0].cpu()
     for i, o in enumerate(outs[1:], 1):
@@ -354,7 +354,7 @@ def test_w4a16_decode_alternating_inputs(gpu, M):
     sets = [T.generate_w4a16_gemm_inputs(M, K, N, G, seed=s, device="cpu") for s in (21, 22)]
     refs = [oracle.w4a16_gemm(A.numpy(), p.numpy(), s.numpy(), z.numpy(), G) for A, p, s, z, G in sets]
     dev = [tuple(t.to(gpu) if isinstance(t, torch.Tensor) else t for t in x) for x in sets]
-    outs = [impl_hip.run(*dev[i % 2]) for i in range(6)]
+    outs = [impl_hip.run(*dev[i % 2], slabs=False) for i in range(6)]
     torch.cuda.synchronize()
     for i, o in enumerate(outs):
         np.testing.assert_allclose(o.cpu().numpy().astype(np.float32), refs[i % 2].astype(np.float32),
@@ -381,13 +381,13 @@ def test_w4a16_decode_graph_survives_workspace_growth(gpu):
     refs = [oracle.w4a16_gemm(A.numpy(), p.numpy(), s.numpy(), z.numpy(), G) for A, p, s, z, G in (small, big)]
     d_small = tuple(t.to(gpu) if isinstance(t, torch.Tensor) else t for t in small)
     d_big = tuple(t.to(gpu) if isinstance(t, torch.Tensor) else t for t in big)
-    impl_hip.run(*d_small)  # allocates the (small) workspace eagerly
+    impl_hip.run(*d_small, slabs=False)  # allocates the (small) workspace eagerly
     torch.cuda.synchronize()
     ws_small = rt._workspaces[key].data_ptr()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        y_graph = impl_hip.run(*d_small)
-    y_big = impl_hip.run(*d_big)  # grows the workspace: a new buffer becomes the cached one
+        y_graph = impl_hip.run(*d_small, slabs=False)
+    y_big = impl_hip.run(*d_big, slabs=False)  # grows the workspace: a new buffer becomes the cached one
     torch.cuda.synchronize()
     assert rt._workspaces[key].data_ptr() != ws_small, "M = 16 should have needed a larger workspace"
     assert any(b.data_ptr() == ws_small for b in rt._retired), "the captured workspace was released"
@@ -396,11 +396,101 @@ def test_w4a16_decode_graph_survives_workspace_growth(gpu):
         torch.cuda.synchronize()
         np.testing.assert_allclose(y_graph.cpu().numpy().astype(np.float32), refs[0].astype(np.float32),
                                    atol=1e-2, rtol=1e-2, err_msg=f"replay {i}")
-        y_big = impl_hip.run(*d_big)
+        y_big = impl_hip.run(*d_big, slabs=False)
         torch.cuda.synchronize()
         np.testing.assert_allclose(y_big.cpu().numpy().astype(np.float32), refs[1].astype(np.float32),
                                    atol=1e-2, rtol=1e-2, err_msg=f"eager call after replay {i}")
     del graph
+
+
+def _slab_layout(packed: np.ndarray) -> np.ndarray:
+    """The slab copy of packed int4 weights [K, N/2] as tb_w4a16_repack_slabs
+    defines it (include/tbhip.h): slab s, unit u, lane l, word b holds the codes
+    of column 64 s + 16 b + l % 16 at rows 32 u + 8 (l / 16) + i, code i at bit
+    (i % 2) * 16 + (i / 2) * 4."""
+    K, half = packed.shape
+    N = 2 * half
+    q = np.empty((K, N), np.uint32)
+    q[:, 0::2] = packed & 15
+    q[:, 1::2] = packed >> 4
+    s = np.arange(N // 64)[:, None, None, None]
+    u = np.arange(K // 32)[None, :, None, None]
+    l = np.arange(64)[None, None, :, None]
+    b = np.arange(4)[None, None, None, :]
+    words = np.zeros((N // 64, K // 32, 64, 4), np.uint32)
+    for i in range(8):
+        words |= q[32 * u + 8 * (l // 16) + i, 64 * s + 16 * b + l % 16] << np.uint32((i % 2) * 16 + (i // 2) * 4)
+    return words.reshape(-1).view(np.uint8)
+
+
+@pytest.mark.parametrize("K,N", [(4096, 11008), (256, 128)])
+def test_w4a16_slab_copy_layout(gpu, K, N):
+    """The GPU slab copy equals the layout restated on the host, byte for byte."""
+    from tilebench_amd import runtime as rt
+
+    _say("w4a16 slab copy layout", K, N)
+    _, p, _, _, _ = T.generate_w4a16_gemm_inputs(1, K, N, 128, seed=K + N, device="cpu")
+    wr = torch.empty(K * N // 2, dtype=torch.uint8, device=gpu)
+    rt.call("tb_w4a16_repack_slabs", p.to(gpu).data_ptr(), wr.data_ptr(), K, N, rt.stream_handle())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(wr.cpu().numpy(), _slab_layout(p.numpy()))
+
+
+@pytest.mark.parametrize("M,K,N,G", [(1, 4096, 11008, 128), (16, 4096, 11008, 128), (5, 4096, 11008, 128),
+                                     (3, 2048, 512, 128), (16, 1024, 256, 64), (2, 1024, 64, 64)])
+def test_w4a16_slab_decode_matches_oracle(gpu, M, K, N, G):
+    """The slab decode (impl_hip's M <= 16 path) against the oracle, three calls
+    in a row bit-identical, and the split-K decode close to it."""
+    from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip
+
+    _say("w4a16 slab decode", M, K, N, G)
+    assert impl_hip.slab_shape_ok(M, N, K, G)
+    A, p, s, z, G = T.generate_w4a16_gemm_inputs(M, K, N, G, seed=7 * M + K, device="cpu")
+    args = (A.to(gpu), p.to(gpu), s.to(gpu), z.to(gpu), G)
+    outs = [impl_hip.run(*args) for _ in range(3)]
+    assert impl_hip.get_last_config()["kernel"] == "w4a16_slab_decode"
+    split = impl_hip.run(*args, slabs=False)
+    torch.cuda.synchronize()
+    ref = oracle.w4a16_gemm(A.numpy(), p.numpy(), s.numpy(), z.numpy(), G)
+    np.testing.assert_allclose(outs[0].cpu().numpy().astype(np.float32), ref.astype(np.float32), atol=1e-2, rtol=1e-2)
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    np.testing.assert_allclose(split.float().cpu().numpy(), outs[0].float().cpu().numpy(), atol=1e-2, rtol=1e-2)
+
+
+def test_w4a16_slab_decode_in_a_graph(gpu):
+    """A graph captured after an eager call replays the slab decode on the copy
+    that call built; a graph captured on weights without a copy runs the
+    split-K decode instead (nothing is built under capture).  Every replay,
+    with eager calls between them, matches the oracle."""
+    from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip
+
+    _say("w4a16 slab decode in a graph")
+    K, N, G = 4096, 11008, 128
+    A, p, s, z, G = T.generate_w4a16_gemm_inputs(1, K, N, G, seed=41, device="cpu")
+    ref = oracle.w4a16_gemm(A.numpy(), p.numpy(), s.numpy(), z.numpy(), G)
+    d = (A.to(gpu), p.to(gpu), s.to(gpu), z.to(gpu), G)
+    fresh = (d[0], d[1].clone(), d[2], d[3], G)   # weights at another address: no copy yet
+    impl_hip.run(*d)
+    torch.cuda.synchronize()
+    g1, g2 = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g1):
+        y1 = impl_hip.run(*d)
+    k1 = impl_hip.get_last_config()["kernel"]
+    with torch.cuda.graph(g2):
+        y2 = impl_hip.run(*fresh)
+    k2 = impl_hip.get_last_config()["kernel"]
+    assert (k1, k2) == ("w4a16_slab_decode", "w4a16_decode")
+    for i in range(3):
+        g1.replay()
+        g2.replay()
+        torch.cuda.synchronize()
+        for y in (y1, y2):
+            np.testing.assert_allclose(y.cpu().numpy().astype(np.float32), ref.astype(np.float32), atol=1e-2,
+                                       rtol=1e-2, err_msg=f"replay {i}")
+        impl_hip.run(*fresh)   # eager: builds the fresh weights' copy between replays
+        torch.cuda.synchronize()
+    del g1, g2
 
 
 # ----------------------------------------------------------------------------- fp8 GEMM

@@ -35,10 +35,18 @@ def _impl(op):
     return importlib.import_module(f"tilebench_amd.benchmarks.operators.{op}.impl_hip")
 
 
+def _same_after_preparation(r):
+    """The first call launched the steady sequence, or that sequence after the
+    one-time build of the W4A16 decode's slab copy."""
+    return r["first_call_identical"] or r["first_call_names"] == ["tb::slabs::slab_repack"] + r["names"]
+
+
 CASES = [
     ("w4a16_gemm", {"M": 4096, "K": 4096, "N": 11008, "group": 128, "dtype": "fp16"},
      [r"tb::w4a16::w4a16_prefill"]),
     ("w4a16_gemm", {"M": 1, "K": 4096, "N": 11008, "group": 128, "dtype": "fp16"},
+     [r"tb::slabs::slab_decode<8, 4>"]),
+    ("w4a16_gemm", {"M": 16, "K": 4096, "N": 11000, "group": 128, "dtype": "fp16"},
      [r"tb::w4a16::w4a16_decode<(false|true)>"]),
     ("matmul_int8", {"M": 1024, "N": 1024, "K": 1024, "dtype": "int8"},
      [r"tb::ntg::unpack_i2_tile", r"tb::ntg::nt_gemm<3, 4, \d+, \d+, \d+, \d+>"]),
@@ -60,7 +68,7 @@ def test_probe_sees_the_kernels_the_shape_selects(gpu, op, case, expected):
     for name, pat in zip(r["names"], expected):
         assert re.fullmatch(pat, name), (name, pat)
     assert r["excluded"] == [], r["excluded"]       # run() itself launches nothing but tb:: kernels
-    assert r["first_call_identical"]
+    assert _same_after_preparation(r)
 
 
 @pytest.mark.parametrize("op", list_operators())
@@ -76,7 +84,7 @@ def test_every_operator_launches_only_backend_kernels(gpu, op):
         r = probe.probe_case(_impl(op), op, case)
         assert r["count"] >= 1 and all(kn.is_backend_kernel(n) for n in r["names"]), r
         assert r["excluded"] == [], r["excluded"]
-        assert r["first_call_identical"], r
+        assert _same_after_preparation(r), r
 
 
 def _rocprof(tmp_path, op, case, mode_args, tag):
@@ -119,7 +127,7 @@ def test_kernel_trace_holds_the_probed_backend_launches(gpu, tmp_path, op, case)
     and first-call set-up included) holds the probe's backend launches, in
     order, and no other tb:: kernel."""
     _say("rocprofv3 --kernel-trace capture", op, case)
-    names = probe.probe_case(_impl(op), op, case)["names"]
+    names = probe.probe_case(_impl(op), op, case)["first_call_names"]  # the workload's run() is a first call
     out = _rocprof(tmp_path, op, case, ["--kernel-trace"], "kt")
     files = sorted(out.rglob("*kernel_trace.csv"))
     assert files, list(out.rglob("*"))

@@ -12,7 +12,10 @@ sequence of each.  One row per pair, with the reference's keys:
      "names":    those launches in launch order (the stems the profilers print),
      "excluded": every other device launch of the call (ATen helpers, runtime
                  copies and fills),
-     "first_call_identical": whether the first call launched the same sequence}
+     "first_call_identical": whether the first call launched the same sequence,
+     "first_call_names": the first call's backend launches (a kernel that keeps
+                per-weight data builds it on its first call: the W4A16 decode's
+                slab copy, tb::slabs::slab_repack)}
 
 With ``--all-cases`` every case of the grid is probed, and each row also lists
 the distinct launch sequences with the cases that produce them (the hip
@@ -74,7 +77,7 @@ def probe_case(impl, op: str, case: dict) -> dict:
     del inputs
     return {"count": len(names), "names": names,
             "excluded": [n for n in launches if kn.is_aux_kernel(n)],
-            "first_call_identical": first_names == names}
+            "first_call_identical": first_names == names, "first_call_names": first_names}
 
 
 def probe_operator(op: str, all_cases: bool = False) -> list[dict]:

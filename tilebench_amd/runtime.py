@@ -38,6 +38,8 @@ SIGNATURES: dict[str, list] = {
     "tb_w4a16_gemm": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64, _c_p],
     "tb_w4a16_workspace_size": [_c_i64, _c_i64, _c_i64, _c_i64, ctypes.POINTER(_c_i64)],
     "tb_w4a16_gemm_noalloc": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p],
+    "tb_w4a16_repack_slabs": [_c_p, _c_p, _c_i64, _c_i64, _c_p],
+    "tb_w4a16_gemm_slabs": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p],
     "tb_moe_w4a16_grouped_gemm": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p],
     "tb_moe_align": [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p],
     "tb_moe_w4a16_gate_up": [_c_p] * 7 + [_c_i64] * 6 + [_c_p],
