@@ -6,9 +6,7 @@
 
 A step is one launch of the operator on one batch of seeded synthetic input
 already resident in HBM.  W untimed warmup steps run eagerly, then one eager
-step on every input copy (per-weight preparation a kernel keeps with its
-weights, the W4A16 decode's slab copy, is built there, as at model load, and
-never inside a graph); then K steps are captured into one hipGraph.  A second graph of the same K steps over other
+step on every input copy; then K steps are captured into one hipGraph.  A second graph of the same K steps over other
 copies of the inputs is replayed first, untimed (as many times as take at
 least WARM_MS = 200 ms and move 2x the MALL), so the GPU is busy and at its
 sustained clock when the timed graph starts; the timed graph is replayed between
@@ -144,7 +142,7 @@ def _w_fp8_quant():
                 step=lambda x: impl_hip.run(*x), kernel="tb::fp8_quant_rows<4>", cpu=cpu)
 
 
-def _w_w4a16(M):
+def _w_w4a16(M, layout="rows"):
     def make():
         from tilebench_amd.data import tensors as T
         from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip, impl_torch
@@ -156,20 +154,47 @@ def _w_w4a16(M):
 
         def cpu():
             rows = min(M, 1024)
-            x = T.generate_w4a16_gemm_inputs(rows, K, N, G, seed=1, device="cpu")
+            x = T.generate_w4a16_gemm_inputs(rows, K, N, G, seed=1, device="cpu", layout=layout)
             work = 2 * rows * K * N if big else nbytes
             return ((lambda: impl_torch.run(*x)), work,
                     f"{rows} of {M} rows (dequantise W, fp32 matmul)" if big else f"full M = {M}")
 
-        return dict(name=f"w4a16_gemm_M{M}",
-                    config={"workload": "w4a16_gemm", "M": M, "K": K, "N": N, "group": G},
+        config = {"workload": "w4a16_gemm", "M": M, "K": K, "N": N, "group": G, "weight_layout": layout}
+        if layout == "slabs":
+            # the layout is a weight format converted once at load; the
+            # conversion is not part of a step (repack_us reports its cost)
+            config["layout_note"] = ("weights converted once to the decode's slab layout "
+                                     "(formats.w4a16_to_slabs) before timing, as at model load")
+        kernel = ("tb::w4a16::w4a16_prefill" if big else
+                  "tb::slabs::slab_decode<8, 4>" if layout == "slabs" else "tb::w4a16::w4a16_decode<false>")
+        name = f"w4a16_gemm_M{M}" + ("_slabs" if layout == "slabs" else "")
+        return dict(name=name, config=config,
                     metric="W4A16 GEMM throughput" if big else "W4A16 decode GEMM HBM throughput",
                     unit="TFLOP/s" if big else "GB/s", dtype="fp16 x int4 -> fp16 (fp32 acc)",
                     bound="mfma" if big else "hbm", peak_key="fp16", bytes=nbytes, flops=flops, out_bytes=2 * M * N,
-                    inputs=lambda: T.generate_w4a16_gemm_inputs(M, K, N, G, seed=1, device="cuda"),
-                    step=lambda x: impl_hip.run(*x),
-                    kernel="tb::w4a16::w4a16_prefill" if big else "tb::slabs::slab_decode<8, 4>", cpu=cpu)
+                    inputs=lambda: T.generate_w4a16_gemm_inputs(M, K, N, G, seed=1, device="cuda", layout=layout),
+                    step=lambda x: impl_hip.run(*x), kernel=kernel, cpu=cpu,
+                    extra=(_slab_repack_us if layout == "slabs" else None))
     return make
+
+
+def _slab_repack_us():
+    """Mean time of one conversion of config 1's weights to the slab layout
+    (tb_w4a16_repack_slabs, the load-time step the slab lines leave out)."""
+    import torch
+    from tilebench_amd import formats
+    from tilebench_amd.data import tensors as T
+
+    _, p, _, _, _ = T.generate_w4a16_gemm_inputs(1, 4096, 11008, 128, seed=1, device="cuda")
+    formats.w4a16_to_slabs(p)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        formats.w4a16_to_slabs(p)
+    e1.record()
+    torch.cuda.synchronize()
+    return {"repack_us": round(e0.elapsed_time(e1) * 100.0, 2)}
 
 
 def _w_fp8_gemm():
@@ -377,6 +402,8 @@ WORKLOADS = {
     "w4a16_gemm_M4096": _w_w4a16(4096),
     "w4a16_gemm_M16": _w_w4a16(16),
     "w4a16_gemm_M1": _w_w4a16(1),
+    "w4a16_gemm_M16_slabs": _w_w4a16(16, "slabs"),
+    "w4a16_gemm_M1_slabs": _w_w4a16(1, "slabs"),
     "int4_dequant": _w_int4_dequant,
     "moe_topk_gating_E64": _w_gating(64),
     "moe_topk_gating_E256": _w_gating(256),
@@ -396,8 +423,9 @@ WORKLOADS = {
 }
 DEFAULT_OP = "w4a16_gemm_M4096"
 #: every BASELINE config besides the headline: measured in the default line's `suite`
-BASELINE_SUITE = ("int4_dequant", "w4a16_gemm_M1", "w4a16_gemm_M16", "fp8_act_quant", "fp8_scaled_gemm",
-                  "moe_topk_gating_E64", "moe_topk_gating_E256", "moe_w4a16_grouped_gemm")
+BASELINE_SUITE = ("int4_dequant", "w4a16_gemm_M1", "w4a16_gemm_M16", "w4a16_gemm_M1_slabs", "w4a16_gemm_M16_slabs",
+                  "fp8_act_quant", "fp8_scaled_gemm", "moe_topk_gating_E64", "moe_topk_gating_E256",
+                  "moe_w4a16_grouped_gemm")
 
 
 # ----------------------------------------------------------------------------- measurement
@@ -411,17 +439,18 @@ def _footprint(x) -> int:
 def input_sets(w, x, steps: int) -> tuple[list, list]:
     """Device copies of the inputs at distinct addresses: (timed sets, warm sets).
 
-    A step moves its inputs plus its output (`traffic`).  With n = ceil(2 x
-    MALL / traffic), a set reused after n other steps has seen 2x the MALL of
-    other traffic in between (the reference evicts the LLC before every timed
+    A step moves its inputs plus its output (`traffic`).  With n =
+    ceil(2 x MALL / traffic) + 1 sets cycling, a set is used again after the
+    n - 1 steps on the other sets, which move at least 2x the MALL of other
+    traffic in between (the reference evicts the LLC before every timed
     launch, tilebench/core/timer.py:81-117, with a 2 x LLC flush).  The timed
-    graph cycles over min(steps, n) sets, so within it every reuse is n steps
-    apart; the warm graph and the eager warmup cycle over n further sets, which
-    the timed sets were cloned before, so when the timed replay starts its sets
-    have not been touched for at least 2x the MALL of traffic either."""
+    graph cycles over min(steps, n) sets (with steps < n no set is used twice);
+    the warm graph and the eager warmup cycle over n further sets, so when the
+    timed replay starts its sets have not been touched for at least 2x the MALL
+    of traffic either."""
     import torch
     traffic = _footprint(x) + w.get("out_bytes", 0)
-    n = max(1, -(-2 * MALL_BYTES // max(traffic, 1)))
+    n = 1 + max(1, -(-2 * MALL_BYTES // max(traffic, 1)))
     n_timed = min(steps, n)
     sets = [x] + [tuple(t.clone() if isinstance(t, torch.Tensor) else t for t in x) for _ in range(n_timed + n - 1)]
     return sets[:n_timed], sets[n_timed:]
@@ -446,9 +475,8 @@ def time_steps(w, timed, warm, steps: int, warmup: int) -> dict:
 
     for i in range(max(1, warmup)):
         w["step"](warm[i % len(warm)])
-    # one eager step on every input set before capture: per-weight preparation
-    # that a kernel keeps with its weights (the W4A16 decode's slab copy) is then
-    # built here, as at model load, and never inside the graphs
+    # one eager step on every input set before capture (no operator keeps
+    # per-input state; this touches every set once, as the timed replay will)
     for x in list(timed) + list(warm):
         w["step"](x)
     torch.cuda.synchronize()
@@ -630,6 +658,8 @@ def measure(name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
     torch.cuda.synchronize()
     t = time_steps(w, timed, warm, steps, warmup)
     out = {"name": w["name"], "w": w, "ms": t["ms"], "timing": t, "roofline": roofline(w, t["ms"])}
+    if w.get("extra"):
+        out["extra"] = w["extra"]()
     del timed, warm
     torch.cuda.empty_cache()
     if with_cpu and w.get("cpu"):
@@ -693,7 +723,7 @@ def main(argv=None) -> int:
             suite[name] = {"metric": r["w"]["metric"], "config": {**r["w"]["config"],
                                                                   "input_sets": r["timing"]["timed_sets"]},
                            "ms": round(r["ms"], 6), "untimed_replays_before": r["timing"]["untimed_replays_before"],
-                           **r["roofline"], "cpu_baseline": r.get("cpu_baseline")}
+                           **r["roofline"], **(r.get("extra") or {}), "cpu_baseline": r.get("cpu_baseline")}
             print(f"[bench] {name}: {r['ms'] * 1e3:.1f} us/step, {r['roofline']['achieved']} "
                   f"{r['roofline']['unit']}", file=sys.stderr, flush=True)
         line["suite"] = suite

@@ -118,12 +118,11 @@ tb_status tb_w4a16_workspace_size(int64_t M, int64_t N, int64_t K, int64_t group
  * K / 32 units of 1 KiB; unit u, lane l, word b (4 bytes at byte
  * ((s * K / 32 + u) * 64 + l) * 16 + 4 b) holds the codes of column
  * 64 s + 16 b + l % 16 at rows 32 u + 8 (l / 16) + i, i = 0..7, code i at bit
- * (i % 2) * 16 + (i / 2) * 4.  Requires K % 32 == 0, N % 64 == 0.  Built once
- * per weight tensor (the caller keeps it with the weights).  No counterpart in
- * the reference, which has no W4A16 operator; it plays the part of the
- * reference's cached column-major fp8 operand
- * (matmul_fp32_fp16_fp8/impl_torch.py:7-18), a per-weight copy in the layout
- * the kernel reads.
+ * (i % 2) * 16 + (i / 2) * 4.  Requires K % 32 == 0, N % 64 == 0.  A weight
+ * format conversion, run once when the weights are loaded (the slab layout is
+ * then the weights' stored form for decode; tilebench_amd.formats.
+ * w4a16_to_slabs); no operator call runs it or keeps its result.  No
+ * counterpart in the reference, which has no W4A16 operator or weight format.
  */
 tb_status tb_w4a16_repack_slabs(const uint8_t* W, uint8_t* Wr, int64_t K, int64_t N, hipStream_t stream);
 
@@ -134,8 +133,9 @@ tb_status tb_w4a16_repack_slabs(const uint8_t* W, uint8_t* Wr, int64_t K, int64_
  * tb_w4a16_gemm's decode (fp32 accumulation of the codes, scale and zero-point
  * applied once per group; results reproducible bit for bit).  Requires
  * N % 64 == 0, G in {64, 128}, K in {1024, 2048, 4096}, K % (16 G) == 0; A
- * and Wr 16-byte aligned.  No counterpart in the reference (see
- * tb_w4a16_repack_slabs).
+ * and Wr 16-byte aligned.  Replaces, for weights stored in the slab layout,
+ * the same reference operator as tb_w4a16_gemm (matmul_fp32_fp16_fp8/
+ * impl_triton.py:124 run(a, b)).
  */
 tb_status tb_w4a16_gemm_slabs(const uint16_t* A, const uint8_t* Wr, const uint16_t* scales, const uint8_t* zeros,
                               uint16_t* Y, int64_t M, int64_t N, int64_t K, int64_t group, hipStream_t stream);

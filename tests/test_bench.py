@@ -44,22 +44,28 @@ def test_more_than_one_gpu_is_refused(capsys):
 
 def test_input_sets_cover_twice_the_mall():
     """Small workloads get enough copies that a timed set is reused only after
-    2x the 256 MiB MALL of other traffic, and the warm sets are distinct."""
+    the steps on the other sets have moved 2x the 256 MiB MALL, and the warm
+    sets are distinct."""
     import torch
     x = (torch.zeros(4 * 1024 * 1024 // 4, dtype=torch.float32), 64, 8)   # 4 MiB of input
     w = {"out_bytes": 1024 * 1024}                                          # + 1 MiB of output per step
     timed, warm = bench.input_sets(w, x, steps=20)
     per = 5 * 1024 * 1024
-    n = -(-2 * bench.MALL_BYTES // per)
-    assert len(timed) == 20 and len(warm) == n
-    assert len(warm) * per >= 2 * bench.MALL_BYTES
+    assert len(timed) == 20            # fewer steps than the rotation: no timed set is used twice
+    assert (len(warm) - 1) * per >= 2 * bench.MALL_BYTES
     ptrs = {s[0].data_ptr() for s in timed + warm}
     assert len(ptrs) == len(timed) + len(warm)
     assert all(s[1:] == (64, 8) for s in timed + warm)
-    # a step that already moves more than 2x the MALL needs no rotation
+    # the headline's traffic (147 MB per step): each set comes back after steps on the
+    # others that move >= 2x the MALL
+    per = 147_156_992
+    x = (torch.zeros(per // 2, dtype=torch.uint8),)
+    timed, warm = bench.input_sets({"out_bytes": per - per // 2}, x, steps=20)
+    assert (len(timed) - 1) * per >= 2 * bench.MALL_BYTES and (len(warm) - 1) * per >= 2 * bench.MALL_BYTES
+    # a step that already moves more than 2x the MALL: two sets alternate
     big = (torch.zeros(1, dtype=torch.uint8),)
     timed, warm = bench.input_sets({"out_bytes": 4 * bench.MALL_BYTES}, big, steps=100)
-    assert len(timed) == 1 and len(warm) == 1
+    assert len(timed) == 2 and len(warm) == 2
 
 
 def test_fp32_matmul_is_priced_as_bf16_mfma_work(monkeypatch):

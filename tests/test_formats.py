@@ -222,3 +222,58 @@ def test_safetensors_round_trip(tmp_path):
     assert torch.equal(f8.wqT, W8.view(torch.uint8)) and torch.equal(f8.sw, torch.full((N,), 0.25))
     with pytest.raises(KeyError):
         F.load_safetensors_layer(path, "l9", "awq")
+
+
+# ----------------------------------------------------------------------------- decode slab layout
+
+
+def slab_byte_and_bit(k: int, n: int, K: int) -> tuple[int, int]:
+    """Where code (k, n) lives in the slab layout, from the map's statement:
+    slab s = n // 64, unit u = k // 32, lane l = 16 * ((k % 32) // 8) + n % 16,
+    word b = (n % 64) // 16, code i = k % 8 at bit (i % 2) * 16 + (i // 2) * 4
+    of that little-endian word."""
+    s, u, i = n // 64, k // 32, k % 8
+    lane = 16 * ((k % 32) // 8) + n % 16
+    b = (n % 64) // 16
+    bit = (i % 2) * 16 + (i // 2) * 4
+    word_byte = ((s * (K // 32) + u) * 64 + lane) * 16 + 4 * b
+    return word_byte + bit // 8, bit % 8
+
+
+@pytest.mark.parametrize("k,n", [(0, 0), (1, 0), (7, 0), (8, 0), (31, 63), (32, 64), (5, 17), (100, 190), (127, 255)])
+def test_slab_layout_places_single_codes(k, n):
+    """A single non-zero code lands at the byte and bit the map names, and
+    nowhere else (K = 128, N = 256)."""
+    K, N = 128, 256
+    q = np.zeros((K, N), np.uint8)
+    q[k, n] = 0xB
+    slabs = F.w4a16_to_slabs(F.pack_columns(torch.from_numpy(q)))
+    assert tuple(slabs.shape) == F.slab_shape(K, N) == (N // 64, K // 32, 1024)
+    flat = slabs.reshape(-1).numpy()
+    byte, bit = slab_byte_and_bit(k, n, K)
+    assert flat[byte] == 0xB << bit
+    assert np.count_nonzero(flat) == 1
+
+
+def test_slab_layout_round_trip_and_product():
+    """Round trip to the packed layout is exact, and the torch reference
+    gives the same product from either layout."""
+    from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_torch
+    from tilebench_amd.data import tensors as T
+
+    A, p, s, z, G = T.generate_w4a16_gemm_inputs(3, 256, 192, 64, seed=9, device="cpu")
+    slabs = F.w4a16_to_slabs(p)
+    assert torch.equal(F.w4a16_from_slabs(slabs), p)
+    assert torch.equal(impl_torch.run(A, slabs, s, z, G), impl_torch.run(A, p, s, z, G))
+    A2, slabs2, s2, z2, _ = T.generate_w4a16_gemm_inputs(3, 256, 192, 64, seed=9, device="cpu", layout="slabs")
+    assert torch.equal(slabs2, slabs) and torch.equal(A2, A)
+
+
+def test_slab_layout_rejects_bad_shapes():
+    with pytest.raises(ValueError):
+        F.w4a16_to_slabs(torch.zeros(48, 32, dtype=torch.uint8))       # K % 32
+    with pytest.raises(ValueError):
+        F.w4a16_to_slabs(torch.zeros(64, 40, dtype=torch.uint8))       # N = 80, N % 64
+    with pytest.raises(ValueError):
+        from tilebench_amd.data import tensors as T
+        T.generate_w4a16_gemm_inputs(17, 256, 128, 64, layout="slabs", device="cpu")

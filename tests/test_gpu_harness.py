@@ -101,3 +101,44 @@ def test_engine_fp8_act_quant_against_the_cpu_reference(gpu):
     _say("engine fp8_act_quant config.yaml")
     rows = engine.run_benchmark_suite("fp8_act_quant", enabled_backends=["hip"])
     _check_rows(rows)
+
+
+def _grid_slices():
+    """The reference's own grids of the analog operators, in slices of at most
+    20 cases (each slice one test, so that every test ends within a minute)."""
+    import yaml
+    from tilebench_amd.data.tensors import expand_cases
+    from tilebench_amd.paths import operator_config
+
+    out = []
+    for op in ("weight_dequant", "dequantize_rowwise", "quantize_global", "matmul_int8", "matmul_fp32_fp16_fp8"):
+        n = len(expand_cases(op, yaml.safe_load(open(operator_config(op)))))
+        out += [(op, list(range(i, min(i + 20, n))), n) for i in range(0, n, 20)]
+    return out
+
+
+@pytest.mark.parametrize("op,idx,total", _grid_slices(), ids=lambda v: v if isinstance(v, str) else None)
+def test_engine_reference_analog_grid(gpu, op, idx, total):
+    """Every case of the reference's grid of each analog operator (weight_dequant
+    60, dequantize_rowwise 20, quantize_global 20, matmul_int8 20,
+    matmul_fp32_fp16_fp8 60) through the engine with impl_hip: each one
+    verifies against impl_torch with the config's tolerance and is timed once."""
+    _say(f"engine {op} grid cases {idx[0]}..{idx[-1]} of {total} (1 sample each)")
+    rows = engine.run_benchmark_suite(op, benchmark_overrides={"repeat": 1, "warmup": 0, "case_indices": idx},
+                                      enabled_backends=["hip"])
+    assert len(rows) == len(idx)
+    for r in rows:
+        assert r["hip_ok"], (op, r["params"], r["dtype"], r["hip_err"])
+        assert r["hip_ms"] > 0, (op, r["params"])
+    print(f"[grid] {op}: {len(rows)} cases verified, hip_ms "
+          f"{min(r['hip_ms'] for r in rows) * 1e3:.1f}..{max(r['hip_ms'] for r in rows) * 1e3:.1f} us", flush=True)
+
+
+def test_engine_w4a16_slab_grid(gpu):
+    """config.yaml's "slabs" grid: the decode shapes on weights the generator
+    converted to the slab layout, verified against impl_torch and timed."""
+    _say("engine w4a16_gemm grid=slabs")
+    rows = engine.run_benchmark_suite("w4a16_gemm", benchmark_overrides={"grid": "slabs"}, enabled_backends=["hip"])
+    _check_rows(rows)
+    assert [r["params"]["M"] for r in rows] == [1, 16]
+    assert all(r["params"]["layout"] == "slabs" and r["hip_config"]["kernel"] == "w4a16_slab_decode" for r in rows)

@@ -9,6 +9,7 @@ import pytest
 import torch
 
 import oracle
+from tilebench_amd import formats
 from tilebench_amd.data import tensors as T
 
 pytestmark = pytest.mark.gpu
@@ -310,9 +311,10 @@ def test_w4a16_gemm_full_prefill(gpu):
 
 def test_w4a16_prefill_192_row_tail(gpu):
     """M = 3000, N = 11008: 12 x 43 = 516 tiles of 256 x 256 would leave a third
-    round of 4 tiles on 256 CUs, so the launch covers the last tile column with
-    16 tiles of 192 rows instead (the last one ragged: rows 2880 .. 2999).
-    Rows from every part, the ragged rows included, against the oracle."""
+    round of 4 tiles on 256 CUs, so the launch covers tile columns 10 .. 42 with
+    16 tiles of 192 rows each instead (the last row of tiles ragged: rows
+    2880 .. 2999).  Rows from every part, the ragged rows included, against the
+    oracle."""
     from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip
 
     M, K, N, G = 3000, 512, 11008, 128
@@ -333,7 +335,7 @@ def test_w4a16_decode_repeat_calls_reuse_workspace(gpu):
     _say("w4a16_gemm decode repeat")
     A, p, s, z, G = T.generate_w4a16_gemm_inputs(16, 4096, 11008, 128, seed=5, device="cpu")
     args = (A.to(gpu), p.to(gpu), s.to(gpu), z.to(gpu), G)
-    outs = [impl_hip.run(*args, slabs=False) for _ in range(3)]
+    outs = [impl_hip.run(*args) for _ in range(3)]
     torch.cuda.synchronize()
     first = outs[0].cpu()
     for i, o in enumerate(outs[1:], 1):
@@ -354,7 +356,7 @@ def test_w4a16_decode_alternating_inputs(gpu, M):
     sets = [T.generate_w4a16_gemm_inputs(M, K, N, G, seed=s, device="cpu") for s in (21, 22)]
     refs = [oracle.w4a16_gemm(A.numpy(), p.numpy(), s.numpy(), z.numpy(), G) for A, p, s, z, G in sets]
     dev = [tuple(t.to(gpu) if isinstance(t, torch.Tensor) else t for t in x) for x in sets]
-    outs = [impl_hip.run(*dev[i % 2], slabs=False) for i in range(6)]
+    outs = [impl_hip.run(*dev[i % 2]) for i in range(6)]
     torch.cuda.synchronize()
     for i, o in enumerate(outs):
         np.testing.assert_allclose(o.cpu().numpy().astype(np.float32), refs[i % 2].astype(np.float32),
@@ -381,13 +383,13 @@ def test_w4a16_decode_graph_survives_workspace_growth(gpu):
     refs = [oracle.w4a16_gemm(A.numpy(), p.numpy(), s.numpy(), z.numpy(), G) for A, p, s, z, G in (small, big)]
     d_small = tuple(t.to(gpu) if isinstance(t, torch.Tensor) else t for t in small)
     d_big = tuple(t.to(gpu) if isinstance(t, torch.Tensor) else t for t in big)
-    impl_hip.run(*d_small, slabs=False)  # allocates the (small) workspace eagerly
+    impl_hip.run(*d_small)  # allocates the (small) workspace eagerly
     torch.cuda.synchronize()
     ws_small = rt._workspaces[key].data_ptr()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        y_graph = impl_hip.run(*d_small, slabs=False)
-    y_big = impl_hip.run(*d_big, slabs=False)  # grows the workspace: a new buffer becomes the cached one
+        y_graph = impl_hip.run(*d_small)
+    y_big = impl_hip.run(*d_big)  # grows the workspace: a new buffer becomes the cached one
     torch.cuda.synchronize()
     assert rt._workspaces[key].data_ptr() != ws_small, "M = 16 should have needed a larger workspace"
     assert any(b.data_ptr() == ws_small for b in rt._retired), "the captured workspace was released"
@@ -396,7 +398,7 @@ def test_w4a16_decode_graph_survives_workspace_growth(gpu):
         torch.cuda.synchronize()
         np.testing.assert_allclose(y_graph.cpu().numpy().astype(np.float32), refs[0].astype(np.float32),
                                    atol=1e-2, rtol=1e-2, err_msg=f"replay {i}")
-        y_big = impl_hip.run(*d_big, slabs=False)
+        y_big = impl_hip.run(*d_big)
         torch.cuda.synchronize()
         np.testing.assert_allclose(y_big.cpu().numpy().astype(np.float32), refs[1].astype(np.float32),
                                    atol=1e-2, rtol=1e-2, err_msg=f"eager call after replay {i}")
@@ -404,10 +406,10 @@ def test_w4a16_decode_graph_survives_workspace_growth(gpu):
 
 
 def _slab_layout(packed: np.ndarray) -> np.ndarray:
-    """The slab copy of packed int4 weights [K, N/2] as tb_w4a16_repack_slabs
-    defines it (include/tbhip.h): slab s, unit u, lane l, word b holds the codes
-    of column 64 s + 16 b + l % 16 at rows 32 u + 8 (l / 16) + i, code i at bit
-    (i % 2) * 16 + (i / 2) * 4."""
+    """The slab layout of packed int4 weights [K, N/2] as include/tbhip.h
+    defines it for tb_w4a16_repack_slabs, restated with numpy fancy indexing:
+    slab s, unit u, lane l, word b holds the codes of column 64 s + 16 b + l % 16
+    at rows 32 u + 8 (l / 16) + i, code i at bit (i % 2) * 16 + (i / 2) * 4."""
     K, half = packed.shape
     N = 2 * half
     q = np.empty((K, N), np.uint32)
@@ -424,32 +426,37 @@ def _slab_layout(packed: np.ndarray) -> np.ndarray:
 
 
 @pytest.mark.parametrize("K,N", [(4096, 11008), (256, 128)])
-def test_w4a16_slab_copy_layout(gpu, K, N):
-    """The GPU slab copy equals the layout restated on the host, byte for byte."""
-    from tilebench_amd import runtime as rt
-
-    _say("w4a16 slab copy layout", K, N)
+def test_w4a16_slab_layout_on_the_gpu(gpu, K, N):
+    """formats.w4a16_to_slabs on a GPU tensor (tb_w4a16_repack_slabs) equals the
+    layout restated on the host, byte for byte, and maps back exactly."""
+    _say("w4a16 slab layout", K, N)
     _, p, _, _, _ = T.generate_w4a16_gemm_inputs(1, K, N, 128, seed=K + N, device="cpu")
-    wr = torch.empty(K * N // 2, dtype=torch.uint8, device=gpu)
-    rt.call("tb_w4a16_repack_slabs", p.to(gpu).data_ptr(), wr.data_ptr(), K, N, rt.stream_handle())
+    wr = formats.w4a16_to_slabs(p.to(gpu))
     torch.cuda.synchronize()
-    np.testing.assert_array_equal(wr.cpu().numpy(), _slab_layout(p.numpy()))
+    assert tuple(wr.shape) == formats.slab_shape(K, N)
+    np.testing.assert_array_equal(wr.cpu().numpy().reshape(-1), _slab_layout(p.numpy()))
+    assert torch.equal(formats.w4a16_from_slabs(wr).cpu(), p)
 
 
+# every slab_decode<UPW, UPG> instance: UPW = K / 512, UPG = G / 32
 @pytest.mark.parametrize("M,K,N,G", [(1, 4096, 11008, 128), (16, 4096, 11008, 128), (5, 4096, 11008, 128),
-                                     (3, 2048, 512, 128), (16, 1024, 256, 64), (2, 1024, 64, 64)])
+                                     (4, 4096, 1024, 64), (9, 2048, 768, 64), (3, 2048, 512, 128),
+                                     (16, 1024, 256, 64), (2, 1024, 64, 64)])
 def test_w4a16_slab_decode_matches_oracle(gpu, M, K, N, G):
-    """The slab decode (impl_hip's M <= 16 path) against the oracle, three calls
-    in a row bit-identical, and the split-K decode close to it."""
+    """The slab decode (weights in the slab layout) against the oracle, three
+    calls in a row bit-identical, and the split-K decode over the packed layout
+    close to it."""
     from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip
 
     _say("w4a16 slab decode", M, K, N, G)
     assert impl_hip.slab_shape_ok(M, N, K, G)
     A, p, s, z, G = T.generate_w4a16_gemm_inputs(M, K, N, G, seed=7 * M + K, device="cpu")
-    args = (A.to(gpu), p.to(gpu), s.to(gpu), z.to(gpu), G)
-    outs = [impl_hip.run(*args) for _ in range(3)]
+    rows = (A.to(gpu), p.to(gpu), s.to(gpu), z.to(gpu), G)
+    slabs = (rows[0], formats.w4a16_to_slabs(rows[1]), rows[2], rows[3], G)
+    outs = [impl_hip.run(*slabs) for _ in range(3)]
     assert impl_hip.get_last_config()["kernel"] == "w4a16_slab_decode"
-    split = impl_hip.run(*args, slabs=False)
+    split = impl_hip.run(*rows)
+    assert impl_hip.get_last_config()["kernel"] == "w4a16_decode"
     torch.cuda.synchronize()
     ref = oracle.w4a16_gemm(A.numpy(), p.numpy(), s.numpy(), z.numpy(), G)
     np.testing.assert_allclose(outs[0].cpu().numpy().astype(np.float32), ref.astype(np.float32), atol=1e-2, rtol=1e-2)
@@ -458,39 +465,83 @@ def test_w4a16_slab_decode_matches_oracle(gpu, M, K, N, G):
     np.testing.assert_allclose(split.float().cpu().numpy(), outs[0].float().cpu().numpy(), atol=1e-2, rtol=1e-2)
 
 
-def test_w4a16_slab_decode_in_a_graph(gpu):
-    """A graph captured after an eager call replays the slab decode on the copy
-    that call built; a graph captured on weights without a copy runs the
-    split-K decode instead (nothing is built under capture).  Every replay,
-    with eager calls between them, matches the oracle."""
+def test_w4a16_slab_layout_refuses_prefill_shapes(gpu):
+    from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip
+
+    A, p, s, z, G = T.generate_w4a16_gemm_inputs(17, 1024, 256, 64, seed=3, device="cpu")
+    with pytest.raises(ValueError, match="decode format"):
+        impl_hip.run(A.to(gpu), formats.w4a16_to_slabs(p.to(gpu)), s.to(gpu), z.to(gpu), G)
+
+
+@pytest.mark.parametrize("layout", ["rows", "slabs"])
+@pytest.mark.parametrize("M", [1, 16, 64])
+def test_w4a16_in_place_weight_update_is_seen(gpu, layout, M):
+    """Weights, scales and zero-points rewritten in place (same tensors, same
+    addresses) between two calls: the second call multiplies by the new
+    values.  run() keeps nothing between calls, so no layout can return a
+    product of the old weights."""
+    from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip
+
+    if layout == "slabs" and M > 16:
+        pytest.skip("the slab layout is a decode format")
+    K, N, G = 4096, 11008, 128
+    _say("w4a16 in-place weight update", layout, M)
+    old = T.generate_w4a16_gemm_inputs(M, K, N, G, seed=51, device="cpu")
+    new = T.generate_w4a16_gemm_inputs(M, K, N, G, seed=52, device="cpu")
+
+    def dev(x):
+        A, p, s, z, g = x
+        p = p.to(gpu)
+        return [A.to(gpu), formats.w4a16_to_slabs(p) if layout == "slabs" else p, s.to(gpu), z.to(gpu), g]
+
+    d_old, d_new = dev(old), dev(new)
+    y_old = impl_hip.run(*d_old)
+    ptrs = [t.data_ptr() for t in d_old[1:4]]
+    for dst, src in zip(d_old[1:4], d_new[1:4]):
+        dst.copy_(src)
+    assert [t.data_ptr() for t in d_old[1:4]] == ptrs
+    y_new = impl_hip.run(*d_old)
+    torch.cuda.synchronize()
+    A = old[0].numpy()
+    for y, (_, p, s, z, _g), what in ((y_old, old, "before"), (y_new, new, "after")):
+        ref = oracle.w4a16_gemm(A, p.numpy(), s.numpy(), z.numpy(), G)
+        np.testing.assert_allclose(y.cpu().numpy().astype(np.float32), ref.astype(np.float32), atol=1e-2, rtol=1e-2,
+                                   err_msg=f"{what} the in-place update")
+
+
+def test_w4a16_slab_decode_in_a_graph_sees_weight_updates(gpu):
+    """A graph captured on slab-layout weights replays the slab decode; the
+    weights rewritten in place between replays (eager work and a sync between
+    them) give the new product on the next replay."""
     from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip
 
     _say("w4a16 slab decode in a graph")
     K, N, G = 4096, 11008, 128
-    A, p, s, z, G = T.generate_w4a16_gemm_inputs(1, K, N, G, seed=41, device="cpu")
-    ref = oracle.w4a16_gemm(A.numpy(), p.numpy(), s.numpy(), z.numpy(), G)
-    d = (A.to(gpu), p.to(gpu), s.to(gpu), z.to(gpu), G)
-    fresh = (d[0], d[1].clone(), d[2], d[3], G)   # weights at another address: no copy yet
+    sets = [T.generate_w4a16_gemm_inputs(1, K, N, G, seed=s, device="cpu") for s in (41, 42)]
+    A = sets[0][0]
+    refs = [oracle.w4a16_gemm(A.numpy(), p.numpy(), s.numpy(), z.numpy(), G) for _, p, s, z, _g in sets]
+    slabs = [formats.w4a16_to_slabs(x[1].to(gpu)) for x in sets]
+    d = (A.to(gpu), slabs[0].clone(), sets[0][2].to(gpu), sets[0][3].to(gpu), G)
+    scales = [x[2].to(gpu) for x in sets]
+    zeros = [x[3].to(gpu) for x in sets]
     impl_hip.run(*d)
     torch.cuda.synchronize()
-    g1, g2 = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g1):
-        y1 = impl_hip.run(*d)
-    k1 = impl_hip.get_last_config()["kernel"]
-    with torch.cuda.graph(g2):
-        y2 = impl_hip.run(*fresh)
-    k2 = impl_hip.get_last_config()["kernel"]
-    assert (k1, k2) == ("w4a16_slab_decode", "w4a16_decode")
-    for i in range(3):
-        g1.replay()
-        g2.replay()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = impl_hip.run(*d)
+    assert impl_hip.get_last_config()["kernel"] == "w4a16_slab_decode"
+    for i in range(4):
+        j = i % 2
+        d[1].copy_(slabs[j])
+        d[2].copy_(scales[j])
+        d[3].copy_(zeros[j])
+        g.replay()
         torch.cuda.synchronize()
-        for y in (y1, y2):
-            np.testing.assert_allclose(y.cpu().numpy().astype(np.float32), ref.astype(np.float32), atol=1e-2,
-                                       rtol=1e-2, err_msg=f"replay {i}")
-        impl_hip.run(*fresh)   # eager: builds the fresh weights' copy between replays
+        np.testing.assert_allclose(y.cpu().numpy().astype(np.float32), refs[j].astype(np.float32), atol=1e-2,
+                                   rtol=1e-2, err_msg=f"replay {i}")
+        impl_hip.run(*d)   # eager work between the replays
         torch.cuda.synchronize()
-    del g1, g2
+    del g
 
 
 # ----------------------------------------------------------------------------- fp8 GEMM

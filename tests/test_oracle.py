@@ -587,3 +587,31 @@ def test_moe_down_closed_form_and_combine_known_answer():
     Yc = np.array([[1, 2], [3, 4], [5, 6], [7, 8]], dtype=np.float16)
     out = oracle.moe_combine(Yc, ids, E)
     assert out.tolist() == [[4, 6], [5, 6]]
+
+
+def test_prefill_plan_closed_form_c():
+    """The W4A16 prefill's launch planner (csrc/prefill_plan.h): its closed-form
+    makespan equals a heap simulation of the greedy schedule on ~3e5 cases, its
+    plans equal the simulation-based planner's, config 1 and the M = 3000 test
+    shape get the plans the GPU tests rely on, and a 65536 x 65536 plan takes
+    under a millisecond; with the closed form planted one start short, the
+    check must fail."""
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ not available")
+    src = os.path.join(ROOT, "tests", "native", "prefill_plan_check.cpp")
+    inc = os.path.join(ROOT, "tilebench_amd", "csrc")
+    out = os.path.join(ROOT, "tests", "native", "_prefill_plan_check")
+    bad = out + "_planted"
+    subprocess.run([gxx, "-O2", "-std=c++17", "-I", inc, src, "-o", out], check=True)
+    subprocess.run([gxx, "-O2", "-std=c++17", "-DPLANT_OFF_BY_ONE", "-I", inc, src, "-o", bad], check=True)
+    try:
+        good = subprocess.run([out], capture_output=True, text=True, timeout=300)
+        assert good.returncode == 0, good.stdout
+        assert "mismatches=0 plan_mismatches=0" in good.stdout
+        planted = subprocess.run([bad], capture_output=True, text=True, timeout=300)
+        assert planted.returncode != 0 and " mismatches=0 " not in planted.stdout
+    finally:
+        for f in (out, bad):
+            if os.path.exists(f):
+                os.remove(f)

@@ -48,6 +48,7 @@
 // contiguous run of tiles, and runs are ordered in groups of 4 tile rows, so
 // the blocks resident on one XCD share A rows and W columns in its L2.
 #include "tb_common.h"
+#include "prefill_plan.h"
 
 #include <algorithm>
 #include <functional>
@@ -1399,50 +1400,11 @@ static tb_status check_dense_args(const char* fn, const uint16_t* A, const uint8
 // Launch of the dense W4A16 GEMM after the checks: the split-K decode kernel
 // for M <= 16 (counters at `workspace`, fp32 partials DEC_COUNTER_BYTES past
 // it), the MFMA prefill kernel otherwise.
-// How the dense prefill covers the output: 256-row tiles over the first
-// n_split tile columns, then 192-row tiles over the rest, chosen so that the
-// work splits into whole rounds of one tile per CU as evenly as it can
-// (a 192-row tile costs about TAIL_COST of a 256-row one).
-struct PrefillPlan {
-  int n_split, n_full, tail_m, tail_n, tail_blocks;
-};
-// measured on MI355X: a round of 192-row tiles takes 0.86 of a round of 256-row ones
-constexpr double TAIL_COST = 0.86;
-static PrefillPlan plan_prefill(int M, int tiles_m, int tiles_n, int cus) {
-  auto makespan = [&](int full, int tail) {
-    // greedy list schedule of `full` unit jobs then `tail` TAIL_COST jobs on `cus` CUs
-    const double rounds_full = (double)(full / cus);
-    const int rem = full % cus;
-    // CUs with rounds_full + 1 full jobs: rem; the tail jobs go to the idle ones first
-    std::vector<double> load((size_t)cus, rounds_full);
-    for (int i = 0; i < rem; ++i) load[(size_t)i] += 1.0;
-    std::make_heap(load.begin(), load.end(), std::greater<double>());
-    for (int i = 0; i < tail; ++i) {
-      std::pop_heap(load.begin(), load.end(), std::greater<double>());
-      load.back() += TAIL_COST;
-      std::push_heap(load.begin(), load.end(), std::greater<double>());
-    }
-    return *std::max_element(load.begin(), load.end());
-  };
-  PrefillPlan p{tiles_n, tiles_m * tiles_n, 0, 0, 0};
-  const int tail_m = (M + 191) / 192;
-  double best = makespan(tiles_m * tiles_n, 0);
-  for (int s = tiles_n - 1; s >= 0; --s) {
-    if ((tiles_m * s) % 8 != 0) continue;
-    const double t = makespan(tiles_m * s, tail_m * (tiles_n - s));
-    if (t < best * 0.97) {
-      best = t;
-      p.n_split = s;
-    }
-  }
-  if (p.n_split < tiles_n) {
-    p.n_full = tiles_m * p.n_split;
-    p.tail_m = tail_m;
-    p.tail_n = tiles_n - p.n_split;
-    p.tail_blocks = (tail_m * p.tail_n + 7) / 8 * 8;
-  }
-  return p;
-}
+// How the dense prefill covers the output (256-row tiles over the first
+// n_split tile columns, 192-row tiles over the rest): tb::plan::plan_prefill,
+// prefill_plan.h, a closed-form evaluation of the greedy schedule per split.
+using tb::plan::PrefillPlan;
+using tb::plan::plan_prefill;
 
 static tb_status launch_dense(const char* fn, const uint16_t* A, const uint8_t* W, const uint16_t* scales,
                               const uint8_t* zeros, uint16_t* Y, int64_t M, int64_t N, int64_t K, int64_t group,

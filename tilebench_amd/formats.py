@@ -197,6 +197,63 @@ def tb_to_awq(w: Int4Weights):
     return pack(unpack_columns(w.packed)), pack(unpack_columns(w.zeros)), w.scales
 
 
+# ----------------------------------------------------------------------------- decode slabs
+
+SLAB_COLS = 64    # columns per slab
+SLAB_UNIT = 32    # K rows per 1 KiB unit
+_SLAB_SHIFT = (0, 16, 4, 20, 8, 24, 12, 28)   # bit of code i within its 32-bit word
+
+
+def slab_shape(K: int, N: int) -> tuple[int, int, int]:
+    """Shape of the slab layout of a [K, N] int4 matrix: uint8 [N/64, K/32, 1024]."""
+    if K % SLAB_UNIT or N % SLAB_COLS or K <= 0 or N <= 0:
+        raise ValueError(f"the slab layout needs K % {SLAB_UNIT} == 0 and N % {SLAB_COLS} == 0 (K={K} N={N})")
+    return (N // SLAB_COLS, K // SLAB_UNIT, 1024)
+
+
+def w4a16_to_slabs(packed: torch.Tensor) -> torch.Tensor:
+    """Packed int4 weights uint8 [K, N/2] -> the decode's slab layout, uint8
+    [N/64, K/32, 1024], a weight format of its own (converted once, at load).
+
+    Slab s holds columns 64 s .. 64 s + 63 as K/32 units of 1 KiB.  In unit u,
+    lane l's 16 bytes are four little-endian 32-bit words; word b holds the
+    codes of column 64 s + 16 b + l % 16 at rows 32 u + 8 (l / 16) + i,
+    i = 0..7, code i at bit (i % 2) * 16 + (i / 2) * 4.  On a GPU tensor the
+    library's tb_w4a16_repack_slabs writes it (one launch); on a CPU tensor the
+    same map is evaluated with torch indexing."""
+    if packed.dtype != torch.uint8 or packed.dim() != 2:
+        raise TypeError("w4a16_to_slabs expects packed uint8 [K, N/2] weights")
+    K, N = packed.shape[0], packed.shape[1] * 2
+    shape = slab_shape(K, N)
+    packed = packed.contiguous()
+    if packed.is_cuda:
+        from tilebench_amd import runtime as rt
+
+        rt.require_device()
+        out = torch.empty(shape, dtype=torch.uint8, device=packed.device)
+        rt.call("tb_w4a16_repack_slabs", packed.data_ptr(), out.data_ptr(), K, N, rt.stream_handle(packed.device))
+        return out
+    # codes q[k, n] with k = 32 u + 8 r + i and n = 64 s + 16 b + c, viewed as [u, r, i, s, b, c]
+    q = unpack_columns(packed).to(torch.int32).reshape(K // 32, 4, 8, N // 64, 4, 16)
+    shifts = torch.tensor(_SLAB_SHIFT, dtype=torch.int32).reshape(1, 1, 1, 1, 1, 8)
+    q = q.permute(3, 0, 1, 5, 4, 2)                  # [s, u, r, c, b, i]: lane l = 16 r + c
+    words = (q << shifts).sum(dim=-1, dtype=torch.int32)
+    return words.contiguous().view(torch.uint8).reshape(shape)
+
+
+def w4a16_from_slabs(slabs: torch.Tensor) -> torch.Tensor:
+    """The inverse of w4a16_to_slabs: uint8 [N/64, K/32, 1024] -> packed
+    uint8 [K, N/2] (torch indexing, any device)."""
+    if slabs.dtype != torch.uint8 or slabs.dim() != 3 or slabs.shape[2] != 1024:
+        raise TypeError("w4a16_from_slabs expects uint8 [N/64, K/32, 1024] slabs")
+    S, U = slabs.shape[0], slabs.shape[1]
+    words = slabs.contiguous().view(torch.int32).reshape(S, U, 4, 16, 4, 1)   # [s, u, r, c, b, 1]
+    shifts = torch.tensor(_SLAB_SHIFT, dtype=torch.int32, device=slabs.device)
+    q = (words >> shifts) & 15                        # [s, u, r, c, b, i]
+    q = q.permute(1, 2, 5, 0, 4, 3).reshape(U * 32, S * 64)   # [u, r, i, s, b, c]
+    return pack_columns(q.to(torch.uint8))
+
+
 # ----------------------------------------------------------------------------- fp8
 
 

@@ -13,9 +13,7 @@ sequence of each.  One row per pair, with the reference's keys:
      "excluded": every other device launch of the call (ATen helpers, runtime
                  copies and fills),
      "first_call_identical": whether the first call launched the same sequence,
-     "first_call_names": the first call's backend launches (a kernel that keeps
-                per-weight data builds it on its first call: the W4A16 decode's
-                slab copy, tb::slabs::slab_repack)}
+     "first_call_names": the first call's backend launches}
 
 With ``--all-cases`` every case of the grid is probed, and each row also lists
 the distinct launch sequences with the cases that produce them (the hip
