@@ -568,9 +568,9 @@ def calibrated_peak(bound: str, peak_key: str | None):
     """The committed calibration (tilebench_amd/data/peak_performance/empirical/
     MI355X.json, written by `python -m tilebench_amd.calibration`) for this
     bound, or None."""
-    from tilebench_amd.core.metrics import load_peak_config
+    from tilebench_amd.core.metrics import load_calibrated_peaks
 
-    cfg = load_peak_config("MI355X")
+    cfg = load_calibrated_peaks("MI355X")
     if bound == "hbm":
         return cfg.get("peak_bw_GBs")
     ck = CALIBRATION_KEY.get(peak_key or "")

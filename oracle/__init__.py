@@ -1,9 +1,10 @@
 """CPU oracle for the ``hip`` backend — TEST INFRASTRUCTURE ONLY.
 
 A plain numpy restatement of what each operator on the hot path computes.  It
-is imported only by ``tests/``, by ``__graft_entry__.smoke()`` (as the checker)
-and by the ``cpu_baseline`` leg of ``bench.py`` (as the timed CPU port).  The
-shipped backend (``tilebench_amd``) never imports it and has no CPU fallback.
+is imported only by ``tests/`` and by ``__graft_entry__.smoke()``, always as the
+checker.  ``bench.py``'s ``cpu_baseline`` times each operator's torch reference
+(``impl_torch.run`` on CPU tensors), not this package.  The shipped backend
+(``tilebench_amd``) never imports it and has no CPU fallback.
 
 Reference anchors (Tilebench has no operator for any of these five configs; the
 oracle follows the semantics of the nearest reference operators and the

@@ -103,8 +103,10 @@ def _filter_rows(E):
     base = lambda: rng.uniform(-5, -1, E).astype(np.float32)
     r = base(); r[np.arange(16) * 4] = 1.0                 # 16 tied candidates: filter path
     rows.append(r)
-    r = base(); r[np.arange(16) * 4] = 1.0; r[1] = 1.0     # 17 candidates: exact path for its wavefront
+    r = base(); r[np.arange(16) * 4] = 1.0; r[1] = 1.0     # 17 candidates: the two-list sort (17..32)
     rows.append(r)
+    r = base(); r[np.arange(16) * 4] = 1.0; r[np.arange(16) * 4 + 1] = 1.0; r[2] = 1.0
+    rows.append(r)                                           # 33 candidates: exact path for its wavefront
     r = base(); r[np.arange(16) * 4] = 0.0; r[8] = -0.0; r[2] = -0.0   # signed zeros at the threshold
     rows.append(r)
     r = base(); r[np.arange(8) * 8] = 2.0; r[np.arange(8) * 8 + 2] = 2.0  # ties inside lanes
@@ -124,9 +126,10 @@ def _filter_rows(E):
 @pytest.mark.parametrize("k", [1, 2, 3, 7, 8])
 def test_gating_filter_paths(gpu, E, k):
     """The filter kernel's shapes (E in {64, 128, 256}, k <= 8): random rows
-    (filter path) mixed with rows that force the exact path for their
-    wavefront (more than 16 candidates, inf, NaN), ties and signed zeros at
-    the threshold, and a ragged row count."""
+    (filter path) mixed with rows that take its two-list sort (17 to 32
+    candidates), rows that force the exact path for their wavefront (more
+    than 32 candidates, inf, NaN), ties and signed zeros at the threshold, and
+    a ragged row count."""
     from tilebench_amd.benchmarks.operators.moe_topk_gating import impl_hip
 
     _say("gating filter paths", E, k)

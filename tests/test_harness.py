@@ -115,6 +115,12 @@ def test_compute_derived_and_roofline():
     assert d["hip"]["pct_peak_tflops"] == pytest.approx(tf / 2500 * 100)
     assert d["hip"]["speedup"] == pytest.approx(4.0)
     assert "speedup" not in d["torch"]
+    # the calibrated peaks (empirical file, "_mma" keys) reported under their own keys
+    d = metrics.compute_derived(res, cfg, {"peak_bw_GBs": 8000.0, "peak_tflops": {"fp16": 2500.0}},
+                                {"peak_bw_GBs": 6500.0, "peak_tflops": {"fp16_mma": 1950.0}})
+    assert d["hip"]["pct_peak_tflops"] == pytest.approx(tf / 2500 * 100)
+    assert d["hip"]["pct_calibrated_peak_tflops"] == pytest.approx(tf / 1950 * 100)
+    assert d["hip"]["pct_calibrated_peak_bw"] == pytest.approx(d["hip"]["bandwidth_GBs"] / 6500 * 100)
     r = metrics.roofline_pct(1e12, 1e9, 1e-3, 8000.0, 2500.0, bound="mfma")
     assert r["frac"] == pytest.approx(1000 / 2500)
     r = metrics.roofline_pct(0, 8e9, 1e-3, 8000.0, None)
@@ -122,6 +128,25 @@ def test_compute_derived_and_roofline():
     # reference rule: the lower ceiling wins (AI = 10 flop/B -> 80 TFLOP/s from HBM)
     r = metrics.roofline_pct(1e11, 1e10, 1e-2, 8000.0, 2500.0)
     assert r["bound_by"] == "hbm" and r["peak"] == pytest.approx(80.0)
+
+
+def test_config_expressions_evaluate_arithmetic_only():
+    ctx = metrics.eval_ctx({"M": 4096, "K": 4096, "N": 11008, "group": 128}, "fp16")
+    assert metrics._eval_expr("2 * M * K + K * N // 2 + (K // group) * N * 2", ctx) == \
+        2 * 4096 * 4096 + 4096 * 11008 // 2 + 32 * 11008 * 2
+    assert metrics._eval_expr("math.ceil(M / 3) + max(K, N) - dtype_size ** 2", ctx) == -(-4096 // 3) + 11008 - 4
+    assert metrics._eval_expr("-M % 5", ctx) == (-4096) % 5
+    for bad in ("__import__('os')", "M.__class__", "open('x')", "unknown * 2", "M / 0", "[M]", ""):
+        assert metrics._eval_expr(bad, ctx) is None, bad
+    assert metrics._eval_expr(None, ctx) is None
+
+
+def test_published_and_calibrated_peak_files():
+    pub, cal = metrics.load_peak_config("MI355X"), metrics.load_calibrated_peaks("MI355X")
+    assert pub["peak_bw_GBs"] == 8000.0 and pub["peak_tflops"]["fp16"] == 2500.0
+    assert pub["peak_tflops"]["fp8_e4m3fn"] == 5000.0
+    assert "fp16_mma" in cal["peak_tflops"] and cal["peak_bw_GBs"] < 8000.0
+    assert metrics.load_peak_config("no-such-gpu") == {}
 
 
 # ----------------------------------------------------------------------------- tensors / configs

@@ -60,26 +60,32 @@ PROTOCOL = {
 # ----------------------------------------------------------------------------- statistics
 
 
-def batch_medians(batches: list[list[float]]) -> list[float]:
-    if not batches or not all(batches):
-        raise ValueError("every batch needs at least one sample")
-    return [statistics.median(b) for b in batches]
+def summarize_batches(batches: list[list[float]]) -> dict:
+    """The protocol's reading of one point's samples: the median of each batch,
+    the point time (the median of those medians, so that no single sample,
+    fastest or slowest, sets it) and the batches' relative spread (range of
+    the batch medians over the point time)."""
+    if len(batches) == 0:
+        raise ValueError("a point needs at least one batch of samples")
+    per_batch = []
+    for i, samples in enumerate(batches):
+        if len(samples) == 0:
+            raise ValueError(f"batch {i} of the point holds no samples")
+        per_batch.append(statistics.median(samples))
+    mid = statistics.median(per_batch)
+    return {"medians": per_batch, "time": mid, "spread": (max(per_batch) - min(per_batch)) / mid}
 
 
 def point_time(batches: list[list[float]]) -> float:
-    """Median over batches of the batch medians."""
-    return statistics.median(batch_medians(batches))
-
-
-def batch_spread(batches: list[list[float]]) -> float:
-    m = batch_medians(batches)
-    return (max(m) - min(m)) / statistics.median(m)
+    return summarize_batches(batches)["time"]
 
 
 def hbm_eligible(working_set: int, llc: int | None, factor: float) -> bool:
-    """Only working sets of at least `factor` x the last-level cache count as
-    HBM; an unknown cache size makes nothing eligible."""
-    return bool(llc) and working_set >= factor * llc
+    """A point measures HBM only if its working set is at least `factor` x the
+    last-level cache; with the cache size unknown no point qualifies."""
+    if llc is None or llc <= 0:
+        return False
+    return working_set >= factor * llc
 
 
 def select_peak(points: list[dict], bandwidth: bool, plateau_tolerance: float = 0.05) -> dict:
@@ -137,9 +143,10 @@ def measure(fn, proto: dict) -> dict:
 
 
 def _point(pid: str, work: float, meas: dict, valid: bool, **extra) -> dict:
-    t = point_time(meas["batches_ms"]) / 1e3
-    return {"id": pid, "work": work, "inner": meas["inner"], "batch_medians_ms": batch_medians(meas["batches_ms"]),
-            "point_time_s": t, "throughput": work / t, "batch_spread": batch_spread(meas["batches_ms"]),
+    summ = summarize_batches(meas["batches_ms"])
+    t = summ["time"] / 1e3
+    return {"id": pid, "work": work, "inner": meas["inner"], "batch_medians_ms": summ["medians"],
+            "point_time_s": t, "throughput": work / t, "batch_spread": summ["spread"],
             "valid": bool(valid), **extra}
 
 

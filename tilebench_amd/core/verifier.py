@@ -83,13 +83,20 @@ def verify(output, reference, atol: float | None = None, rtol: float | None = No
     return _verify_single(output, reference, atol=atol, rtol=rtol)
 
 
+def _settings_on(verify_cfg: dict, arch: str | None) -> dict:
+    """A config's verify: section with its arch_overrides entry for `arch`
+    laid over it (the override wins for every key it names)."""
+    merged = dict(verify_cfg)
+    merged.update((verify_cfg.get("arch_overrides") or {}).get(arch) or {})
+    return merged
+
+
 def config_tolerance(verify_cfg: dict, arch: str | None) -> tuple[float | None, float | None]:
-    """(atol, rtol) of a config's verify: section on `arch`; arch_overrides win."""
-    cfg = {**verify_cfg, **(verify_cfg.get("arch_overrides") or {}).get(arch, {})}
-    return (float(cfg["atol"]) if "atol" in cfg else None,
-            float(cfg["rtol"]) if "rtol" in cfg else None)
+    """(atol, rtol) of a config's verify: section on `arch`; a value the
+    section does not give is None (the output dtype's default then applies)."""
+    s = _settings_on(verify_cfg, arch)
+    return tuple(None if s.get(k) is None else float(s[k]) for k in ("atol", "rtol"))
 
 
 def config_per_output(verify_cfg: dict, arch: str | None):
-    cfg = {**verify_cfg, **(verify_cfg.get("arch_overrides") or {}).get(arch, {})}
-    return cfg.get("per_output")
+    return _settings_on(verify_cfg, arch).get("per_output")

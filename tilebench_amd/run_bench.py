@@ -10,7 +10,8 @@ for the backends this package ships: for each case it generates the inputs,
 runs the torch reference, then runs, verifies and times the selected
 backends (tilebench_amd.core.engine.run_benchmark_suite with the real
 hipGraph/hipEvent timer), and prints one line per case with the derived
-metrics against the calibrated MI355X peaks.
+metrics: % of the device's published peaks (pct_peak_*, the reference's
+definition) and of the peaks calibrated on the box (pct_calibrated_peak_*).
 """
 from __future__ import annotations
 
@@ -61,9 +62,13 @@ def main(argv=None) -> int:
     backends = parse_backends(args.tile_language)
     rows = engine.run_benchmark_suite(args.operator, benchmark_overrides=over, enabled_backends=backends)
     cfg = yaml.safe_load(open(operator_config(args.operator)))
-    peak = metrics.load_peak_config("MI355X")
+    from tilebench_amd import calibration
+    gpu = calibration.gpu_model(calibration.environment())
+    peak, calibrated = metrics.load_peak_config(gpu), metrics.load_calibrated_peaks(gpu)
+    print(f"# {gpu}: % of peak against {'the published peaks' if peak else 'no published peak file'}"
+          f"{', pct_calibrated_* against the calibrated peaks' if calibrated else ''}", flush=True)
     for r in rows:
-        r["derived"] = metrics.compute_derived(r, cfg.get("metrics", {}), peak)
+        r["derived"] = metrics.compute_derived(r, cfg.get("metrics", {}), peak, calibrated)
         line = [f"{k}={v}" for k, v in r["params"].items()] + [f"dtype={r['dtype']}",
                                                                  f"torch_ms={_fmt(r['torch_ms'])}"]
         for b in backends:
@@ -76,7 +81,7 @@ def main(argv=None) -> int:
                 line.append(f"{b}_GBs={_fmt(d['bandwidth_GBs'], '.1f')}")
             if "tflops" in d:
                 line.append(f"{b}_TFLOPS={_fmt(d['tflops'], '.1f')}")
-            for key in ("pct_peak_bw", "pct_peak_tflops"):
+            for key in ("pct_peak_bw", "pct_peak_tflops", "pct_calibrated_peak_bw", "pct_calibrated_peak_tflops"):
                 if key in d:
                     line.append(f"{b}_{key}={_fmt(d[key], '.1f')}")
             if not r[f"{b}_ok"]:
