@@ -218,6 +218,30 @@ def _w_fp8_gemm():
                 step=lambda x: impl_hip.run(*x), kernel="tb::fp8gemm::fp8_gemm_kernel", cpu=cpu)
 
 
+def _w_fp8_block_gemm():
+    from tilebench_amd.data import tensors as T
+    from tilebench_amd.benchmarks.operators.fp8_block_scaled_gemm import impl_hip, impl_torch
+
+    M = N = K = 8192
+    flops = 2 * M * N * K
+    nbytes = M * K + N * K + 4 * M * (K // 128) + 4 * ((N + 127) // 128) * (K // 128) + 2 * M * N
+
+    def cpu():
+        rows = 1024
+        x = T.generate_fp8_block_scaled_gemm_inputs(rows, N, K, seed=2, device="cpu")
+        return ((lambda: impl_torch.run(*x)), 2 * rows * N * K,
+                f"{rows} of {M} rows (block-dequantised operands, fp32 matmul)")
+
+    return dict(name="fp8_block_scaled_gemm", config={"workload": "fp8_block_scaled_gemm", "M": M, "N": N, "K": K,
+                                                      "block": 128},
+                metric="block-scaled fp8 GEMM throughput (128 x 128 weight blocks, per-token 128-channel "
+                       "activation blocks)",
+                unit="TFLOP/s", dtype="e4m3 x e4m3 -> bf16 (fp32 acc)", bound="mfma", peak_key="fp8", bytes=nbytes,
+                flops=flops, out_bytes=2 * M * N,
+                inputs=lambda: T.generate_fp8_block_scaled_gemm_inputs(M, N, K, seed=2, device="cuda"),
+                step=lambda x: impl_hip.run(*x), kernel="tb::fp8blk::fp8_block_gemm", cpu=cpu)
+
+
 def _w_grouped():
     from tilebench_amd.data import tensors as T
     from tilebench_amd.benchmarks.operators.moe_w4a16_grouped_gemm import impl_hip, impl_torch
@@ -410,6 +434,7 @@ WORKLOADS = {
     "moe_topk_gating_ref_grid": _w_gating_reference_grid,
     "fp8_act_quant": _w_fp8_quant,
     "fp8_scaled_gemm": _w_fp8_gemm,
+    "fp8_block_scaled_gemm": _w_fp8_block_gemm,
     "moe_w4a16_grouped_gemm": _w_grouped,
     "fused_moe_w4a16": _w_fused_moe,
     "weight_dequant": _w_weight_dequant,
@@ -425,7 +450,7 @@ DEFAULT_OP = "w4a16_gemm_M4096"
 #: every BASELINE config besides the headline: measured in the default line's `suite`
 BASELINE_SUITE = ("int4_dequant", "w4a16_gemm_M1", "w4a16_gemm_M16", "w4a16_gemm_M1_slabs", "w4a16_gemm_M16_slabs",
                   "fp8_act_quant", "fp8_scaled_gemm", "moe_topk_gating_E64", "moe_topk_gating_E256",
-                  "moe_w4a16_grouped_gemm")
+                  "moe_w4a16_grouped_gemm", "fp8_block_scaled_gemm")
 
 
 # ----------------------------------------------------------------------------- measurement

@@ -247,6 +247,31 @@ tb_status tb_fp8_scaled_gemm(const uint8_t* Aq, const uint8_t* WqT, const float*
                              int64_t M, int64_t N, int64_t K, hipStream_t stream);
 
 /*
+ * Block-scaled fp8 (the 128 x 128 weight-scale blocks of DeepSeek-V3-style
+ * fp8 checkpoints, "weight_scale_inv" [ceil(N/128), K/128]):
+ *
+ * tb_fp8_act_quant_blocks: per token and per block of 128 input channels,
+ *   sa[kb, m] = fp32(max_{k in block kb} |A[m,k]|) / 448 and
+ *   Aq[m, k] = e4m3(RN32(fp32(A[m,k]) / sa[k/128, m])), the arithmetic of
+ *   tb_fp8_act_quant on each block.  A fp16 [M, K]; Aq uint8 [M, K]; sa fp32
+ *   [K/128, M] (block-major, M contiguous).  Requires K % 128 == 0, A 16-byte
+ *   and Aq 8-byte aligned.
+ * tb_fp8_block_gemm: Y bf16 [M, N] =
+ *   bf16( sum_kb (sa[kb, m] * sw[n/128, kb]) * sum_{k in block kb} Aq[m,k] * WqT[n,k] ),
+ *   the block sums in fp32 on the e4m3 matrix cores, scaled and added in fp32
+ *   in block order, one RNE rounding.  WqT uint8 [N, K]; sw fp32
+ *   [ceil(N/128), K/128] row-major.  Requires K % 128 == 0, K <= 65536,
+ *   N % 8 == 0, each operand < 2 GiB, Aq / WqT 16-byte and Y 8-byte aligned.
+ * Replace: the reference's block-scaled weight dequantisation
+ *   (weight_dequant/impl_torch.py:4-8, X * S[i//T, j//T] with T = 128) fused
+ *   into its fp8 GEMM (matmul_fp32_fp16_fp8/impl_triton.py:124 run(a, b)).
+ */
+tb_status tb_fp8_act_quant_blocks(const uint16_t* A, uint8_t* Aq, float* sa, int64_t M, int64_t K,
+                                  hipStream_t stream);
+tb_status tb_fp8_block_gemm(const uint8_t* Aq, const uint8_t* WqT, const float* sa, const float* sw, uint16_t* Y,
+                            int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+/*
  * The reference's own elementwise dequantisation / quantisation operators.
  * Each product is formed in fp32 and rounded once to the output type (RNE), in
  * the PyTorch reference's order of operations (bit-identical results).

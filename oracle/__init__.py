@@ -20,6 +20,10 @@ BASELINE config text):
                       saturation).
 * fp8 scaled GEMM   — matmul_fp32_fp16_fp8/impl_torch.py:10-26 (_scaled_mm, bf16 out)
                       with per-row / per-column scales instead of unit scales.
+* block-scaled fp8  — weight_dequant/impl_torch.py:4-8 (X * S[i//T, j//T], T = 128:
+                      the 128 x 128 weight-scale map) fused into the fp8 GEMM above,
+                      with activations quantised per token and per 128 channels by
+                      the fp8 act quant rule applied to each block.
 * MoE gating        — moe_topk_gating/impl_torch.py:4-20 (topk, softmax over the k
                       values in fp32, int32 indices) with ties -> lowest index.
 * weight_dequant    — weight_dequant/impl_torch.py:4-8; dequantize_rowwise —
@@ -48,6 +52,8 @@ from .core import (  # noqa: F401
     e4m3_to_f32,
     f32_to_bf16_bits,
     fp8_act_quant,
+    fp8_act_quant_blocks,
+    fp8_block_gemm,
     fp8_scaled_gemm,
     int4_dequant,
     moe_topk_gating,

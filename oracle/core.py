@@ -153,6 +153,49 @@ def fp8_scaled_gemm(Aq: np.ndarray, Wq: np.ndarray, sa: np.ndarray, sw: np.ndarr
     return f32_to_bf16_bits(y.astype(np.float32))
 
 
+def fp8_act_quant_blocks(A: np.ndarray, block: int = 128):
+    """Per-token, per-block fp8 quantisation of fp16 A [M, K] (K % block == 0)
+    -> (codes uint8 [M, K], sa fp32 [K/block, M], block-major).
+
+    Each block of `block` consecutive elements of a row is quantised exactly as
+    fp8_act_quant quantises a row: sa = fp32(max |block|) / 448, codes =
+    e4m3(fp32(A) / sa), an all-zero block giving sa = 0 and 0xFF codes."""
+    A = np.asarray(A, dtype=np.float16)
+    M, K = A.shape
+    if K % block:
+        raise ValueError(f"K = {K} is not a multiple of the block size {block}")
+    codes, sa = fp8_act_quant(A.reshape(M * (K // block), block))
+    return codes.reshape(M, K), np.ascontiguousarray(sa.reshape(M, K // block).T)
+
+
+def fp8_block_gemm(Aq: np.ndarray, WqT: np.ndarray, sa: np.ndarray, sw: np.ndarray, block: int = 128) -> np.ndarray:
+    """Y bf16 bits [M, N] = bf16( sum_kb s[kb, m, n] * P_kb[m, n] ) with
+    P_kb = sum_{k in block kb} e4m3(Aq[m,k]) * e4m3(WqT[n,k]) and
+    s = fp32(sa[kb, m] * sw[n // block, kb]).
+
+    Aq [M, K] and WqT [N, K] are e4m3 codes, sa fp32 [K/block, M], sw fp32
+    [ceil(N/block), K/block].  Each P_kb is exact in float64 (128 products of
+    4-bit significands spanning at most 2^-18 .. 2^18); the scaled terms are
+    summed in float64 in block order and the sum is rounded once to bf16."""
+    a = e4m3_to_f32(Aq).astype(np.float64)
+    w = e4m3_to_f32(WqT).astype(np.float64)
+    M, K = a.shape
+    N = w.shape[0]
+    sa = np.asarray(sa, np.float32)
+    sw = np.asarray(sw, np.float32)
+    nkb = K // block
+    if K % block or sa.shape != (nkb, M) or sw.shape != ((N + block - 1) // block, nkb):
+        raise ValueError("fp8_block_gemm: operand / scale shapes do not match")
+    col_block = np.arange(N) // block
+    acc = np.zeros((M, N), np.float64)
+    for kb in range(nkb):
+        ks = slice(kb * block, (kb + 1) * block)
+        P = a[:, ks] @ w[:, ks].T
+        s = (sa[kb][:, None] * sw[col_block, kb][None, :]).astype(np.float32)
+        acc += s.astype(np.float64) * P
+    return f32_to_bf16_bits(acc.astype(np.float32))
+
+
 # ----------------------------------------------------------------------------- W4A16 GEMMs
 
 

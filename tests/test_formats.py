@@ -179,10 +179,32 @@ def test_fp8_scale_conventions():
     # weight_scale_inv is the dequantisation multiplier too (DeepSeek-V3 / FineGrainedFP8)
     b = F.fp8_checkpoint_to_tb(W, weight_scale_inv=torch.tensor(4.0))
     assert torch.equal(b.sw, torch.full((6,), 4.0))
-    with pytest.raises(NotImplementedError, match="block"):
+    with pytest.raises(ValueError, match="blocks"):
         F.fp8_checkpoint_to_tb(W, torch.ones(1, 1, 2))
     with pytest.raises(ValueError):
         F.fp8_checkpoint_to_tb(W)
+
+
+def test_fp8_block_scales_select_the_block_gemm():
+    """A DeepSeek-V3-style layer (weight [N, K], weight_scale_inv one fp32 per
+    128 x 128 tile, ragged in N) converts to the block GEMM's operands, and
+    dequantising through them is the reference's block map
+    (weight_dequant: X * S[i//128, j//128])."""
+    N, K = 300, 384
+    g = torch.Generator().manual_seed(11)
+    W = (torch.randn(N, K, generator=g) * 4).to(torch.float8_e4m3fn)
+    inv = torch.rand(3, 3, generator=g) + 0.1
+    f = F.fp8_checkpoint_to_tb(W, weight_scale_inv=inv)
+    assert isinstance(f, F.Fp8BlockWeights) and f.block == 128
+    assert torch.equal(f.wqT, W.view(torch.uint8)) and torch.equal(f.sw, inv)
+    back = f.wqT.view(torch.float8_e4m3fn).to(torch.float32) * f.sw.repeat_interleave(128, 0)[:N].repeat_interleave(128, 1)
+    ref = oracle.weight_dequant(W.to(torch.float32).numpy(), inv.numpy(), 128, "fp32")
+    assert np.array_equal(back.numpy(), ref)
+    with pytest.raises(ValueError, match="K % 128"):
+        F.fp8_checkpoint_to_tb(torch.zeros(256, 200, dtype=torch.uint8), torch.ones(2, 2))
+    # one K block: [ceil(N/128), 1] is still a block map when it is not [N, 1]
+    f1 = F.fp8_checkpoint_to_tb(torch.zeros(256, 128, dtype=torch.uint8), torch.ones(2, 1))
+    assert isinstance(f1, F.Fp8BlockWeights) and tuple(f1.sw.shape) == (2, 1)
 
 
 def test_fp8_scale_inv_round_trip():

@@ -28,6 +28,8 @@ CASES = [
     ("w4a16_gemm", {"M": 300, "K": 512, "N": 1024, "group": 128, "dtype": "fp16"}),
     ("fp8_act_quant", {"M": 256, "K": 4096, "dtype": "fp16"}),
     ("fp8_scaled_gemm", {"M": 512, "N": 512, "K": 1024}),
+    ("fp8_act_quant_blocks", {"M": 256, "K": 4096, "dtype": "fp16"}),
+    ("fp8_block_scaled_gemm", {"M": 512, "N": 384, "K": 1024}),
     ("moe_topk_gating", {"M": 1024, "E": 64, "k": 8, "dtype": "fp32"}),
     ("moe_topk_gating", {"M": 1024, "E": 256, "k": 8, "dtype": "fp32"}),
     ("moe_topk_gating", {"M": 1024, "E": 128, "k": 2, "dtype": "fp16"}),

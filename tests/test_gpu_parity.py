@@ -249,7 +249,8 @@ def test_fp8_quant_matches_oracle(gpu, M, K):
 
 
 def test_fp8_quant_special_rows(gpu):
-    """Zero row, a row whose max maps to exactly 448, subnormal fp16 inputs, +-65504, signed zeros."""
+    """Zero row, a row whose max maps to exactly 448, subnormal fp16 inputs, +-65504, signed zeros,
+    rows holding inf and NaN (the IEEE quotients of the CPU reference)."""
     from tilebench_amd.benchmarks.operators.fp8_act_quant import impl_hip
 
     _say("fp8_act_quant special rows")
@@ -266,6 +267,12 @@ def test_fp8_quant_special_rows(gpu):
     A[5] = np.arange(K, dtype=np.uint16).view(np.float16)                    # every bit pattern below 0x1000
     A[6] = (np.arange(K, dtype=np.uint32) * 15 + 0x3C00).astype(np.uint16).view(np.float16)
     A[6][~np.isfinite(A[6])] = 1.0
+    A[7, 3] = np.inf                                                        # row max inf: +-0 codes, inf -> NaN
+    A[7, 4] = -np.inf
+    A = np.concatenate([A, rng.standard_normal((2, K)).astype(np.float16)])
+    A[8, 11] = np.nan                                                       # a NaN row: NaN codes
+    A[9, 12] = np.uint16(0xFE00).view(np.float16)                           # a NaN with the sign bit set
+    A[9, 13] = -np.inf
     q, sa = impl_hip.run(torch.from_numpy(A).to(gpu))
     torch.cuda.synchronize()
     rq, rsa = oracle.fp8_act_quant(A)

@@ -273,6 +273,112 @@ def test_fp8_scaled_gemm_identity():
     assert np.array_equal(oracle.fp8_scaled_gemm(Aq, Wq, sa, sw), expect)
 
 
+def _bf16_from_fraction(x: Fraction) -> float:
+    """Round an exact rational to bf16 (nearest, ties to even) without numpy:
+    scale to the 8-bit significand grid of its binade and round the integer."""
+    if x == 0:
+        return 0.0
+    sign = -1 if x < 0 else 1
+    x = abs(x)
+    e = math.floor(math.log2(x.numerator) - math.log2(x.denominator))
+    while Fraction(2) ** e > x:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= x:
+        e += 1
+    step = Fraction(2) ** (e - 7)
+    q, r = divmod(x, step)
+    q = int(q)
+    if r * 2 > step or (r * 2 == step and q % 2 == 1):
+        q += 1
+    return sign * float(q * step)
+
+
+def test_fp8_block_gemm_exact_rationals():
+    """Tiny shapes (two K blocks, a ragged column block): every output equals
+    the exact rational sum over blocks of fp32(sa * sw) * P_kb, rounded once to
+    bf16 (computed with Fractions, independently of numpy's arithmetic)."""
+    rng = np.random.default_rng(21)
+    M, N, K = 3, 130, 256
+    Aq = rng.integers(0, 0x7F, (M, K), dtype=np.uint8) | (rng.integers(0, 2, (M, K), dtype=np.uint8) << 7)
+    Wt = rng.integers(0, 0x7F, (N, K), dtype=np.uint8) | (rng.integers(0, 2, (N, K), dtype=np.uint8) << 7)
+    sa = (rng.random((2, M)) + 0.25).astype(np.float32)
+    sw = (rng.random((2, 2)) * 0.01 + 1e-3).astype(np.float32)
+    Y = oracle.bf16_bits_to_f32(oracle.fp8_block_gemm(Aq, Wt, sa, sw))
+    a, w = oracle.e4m3_to_f32(Aq), oracle.e4m3_to_f32(Wt)
+    for m, n in itertools.product(range(M), (0, 1, 64, 127, 128, 129)):
+        total = Fraction(0)
+        for kb in range(2):
+            p = sum(Fraction(float(a[m, k])) * Fraction(float(w[n, k])) for k in range(128 * kb, 128 * kb + 128))
+            s = Fraction(float(np.float32(sa[kb, m]) * np.float32(sw[n // 128, kb])))
+            total += s * p
+        ref = _bf16_from_fraction(total)
+        assert Y[m, n] == ref or abs(Y[m, n] - ref) <= abs(ref) * 2 ** -7, (m, n, Y[m, n], ref)
+
+
+def test_fp8_block_gemm_reduces_to_the_row_column_scaled_gemm():
+    """Scales that do not vary over K blocks (sa[kb, m] = r[m], sw[nb, kb] =
+    c[nb]) make the block formula the row/column-scaled GEMM with sw[n] =
+    c[n // 128]: the two oracles agree to one bf16 ulp."""
+    rng = np.random.default_rng(22)
+    M, N, K = 5, 200, 384
+    Aq = rng.integers(0, 0x7E, (M, K), dtype=np.uint8)
+    Wt = rng.integers(0, 0x7E, (N, K), dtype=np.uint8) | (rng.integers(0, 2, (N, K), dtype=np.uint8) << 7)
+    r = (rng.random(M) + 0.5).astype(np.float32)
+    c = (rng.random(2) * 0.01 + 1e-3).astype(np.float32)
+    block = oracle.bf16_bits_to_f32(oracle.fp8_block_gemm(Aq, Wt, np.tile(r, (3, 1)), np.repeat(c[:, None], 3, 1)))
+    rowcol = oracle.bf16_bits_to_f32(oracle.fp8_scaled_gemm(Aq, Wt.T, r, c[np.arange(N) // 128]))
+    np.testing.assert_allclose(block, rowcol, rtol=2 ** -7, atol=0)
+
+
+def test_fp8_block_gemm_matches_the_reference_block_dequant():
+    """The product of the operands dequantised by the reference's block-scale
+    map (oracle.weight_dequant, weight_dequant/impl_torch.py:4-8, T = 128) for
+    the weights [N, K] and per token and block for the activations, in
+    float64: within the GEMM tolerance (1e-2), and a transposed weight scale
+    map is caught."""
+    rng = np.random.default_rng(23)
+    M, N, K = 16, 256, 512
+    Aq = rng.integers(0, 0x7E, (M, K), dtype=np.uint8) | (rng.integers(0, 2, (M, K), dtype=np.uint8) << 7)
+    Wt = rng.integers(0, 0x7E, (N, K), dtype=np.uint8) | (rng.integers(0, 2, (N, K), dtype=np.uint8) << 7)
+    sa = (rng.random((4, M)) + 0.5).astype(np.float32)
+    sw = (rng.random((2, 4)) * 0.01 + 1e-3).astype(np.float32)
+    w_deq = oracle.weight_dequant(oracle.e4m3_to_f32(Wt), sw, 128, "fp32").astype(np.float64)
+    a_deq = oracle.e4m3_to_f32(Aq).astype(np.float64) * np.repeat(sa.T, 128, axis=1)
+    ref = a_deq @ w_deq.T
+    got = oracle.bf16_bits_to_f32(oracle.fp8_block_gemm(Aq, Wt, sa, sw))
+    np.testing.assert_allclose(got, ref, atol=1e-2, rtol=1e-2)
+    bad = oracle.bf16_bits_to_f32(oracle.fp8_block_gemm(Aq, Wt, sa, np.ascontiguousarray(sw[::-1])))
+    assert not np.allclose(bad, ref, atol=1e-2, rtol=1e-2)
+
+
+def test_fp8_act_quant_blocks_known_answers():
+    """Hand-built blocks: a block whose maximum is 896 has sa = 2 and codes of
+    896 -> 448 (0x7E) and 2 -> 1.0 (0x38); an all-zero block has sa = 0 and
+    0xFF codes; sa is block-major (sa[kb, m]); and the torch reference agrees
+    bit for bit on config 2's outlier distribution."""
+    from tilebench_amd.benchmarks.operators.fp8_act_quant_blocks import impl_torch
+    from tilebench_amd.data import tensors as T
+
+    A = np.zeros((2, 384), np.float16)
+    A[0, 5] = 896.0
+    A[0, 6] = 2.0
+    A[0, 7] = -2.0
+    A[1, 128:256] = np.arange(128, dtype=np.float16) * np.float16(0.5)     # max 63.5
+    A[1, 300] = -7.0
+    codes, sa = oracle.fp8_act_quant_blocks(A)
+    assert sa.shape == (3, 2)
+    assert sa[0, 0] == np.float32(2.0) and sa[1, 0] == 0 and sa[2, 0] == 0
+    assert sa[0, 1] == 0 and sa[1, 1] == np.float32(63.5) / np.float32(448) and sa[2, 1] == np.float32(7.0) / 448
+    assert codes[0, 5] == 0x7E and codes[0, 6] == 0x38 and codes[0, 7] == 0xB8
+    assert (codes[0, 128:] == 0xFF).all() and (codes[1, :128] == 0xFF).all()
+    assert codes[1, 255] == 0x7E and codes[1, 300] == 0xFE
+    X = T.fp8_activations(96, 1024, seed=4)
+    Aq, s = impl_torch.run(X)
+    c2, s2 = oracle.fp8_act_quant_blocks(X.numpy())
+    assert np.array_equal(Aq.view(torch.uint8).numpy(), c2)
+    assert np.array_equal(s.numpy().view(np.uint32), s2.view(np.uint32))
+
+
 def test_w4a16_gemm_brute_force_float64():
     rng = np.random.default_rng(9)
     M, K, N, G = 3, 8, 6, 4

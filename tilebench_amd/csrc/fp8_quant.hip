@@ -34,57 +34,11 @@
 //                                   the exponent is the correct rounding result
 //                                   (448 < |q| <= 464 rounds to 448, above -> NaN)
 #include "tb_common.h"
+#include "fp8_codec.h"
 
 #pragma clang fp contract(off)
 
 namespace tb {
-
-// The refinement yields +0 for x = -0 (fma(+0, y, -0) = +0); sa and y are
-// positive, so the quotient always carries the sign of x and copysign restores it.
-__device__ __forceinline__ float quotient(float x, float sa, float y) {
-  const float q0 = x * y;
-  const float r = __builtin_fmaf(-q0, sa, x);
-  return __builtin_copysignf(__builtin_fmaf(r, y, q0), x);
-}
-
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, 64));
-  return v;
-}
-
-// Eight fp16 values -> eight e4m3 codes of x / sa.  `m` is the row's largest
-// magnitude as fp16 bits.  For a finite, non-zero row every quotient lies in
-// [-448, 448] (up to one fp32 rounding), where the hardware conversion
-// v_cvt_pk_fp8_f32 rounds exactly as the integer encoder e4m3_code (checked on
-// the device against the torch-pinned CPU oracle for all e4m3 values, every
-// rounding midpoint +-1 fp32 ulp, the subnormal range, signed zeros and 3*10^6
-// random values with |x| <= 464: no difference).  A zero row gives 0xFF codes
-// (x86's 0/0); rows holding inf or NaN take the integer encoder.
-__device__ __forceinline__ u32x2 quantize_chunk(const u32x4& x, float sa, float y, uint32_t m) {
-  float q[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint16_t h = (uint16_t)((x[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
-    q[j] = quotient((float)__builtin_bit_cast(_Float16, h), sa, y);
-  }
-  u32x2 o;
-  if (m == 0) {
-    o[0] = o[1] = 0xFFFFFFFFu;
-  } else if (m < 0x7C00u) {
-    o[0] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
-    o[0] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], (int)o[0], true);
-    o[1] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], 0, false);
-    o[1] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[6], q[7], (int)o[1], true);
-  } else {
-    uint32_t c[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) c[j] = e4m3_code(q[j]);
-    o[0] = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-    o[1] = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-  }
-  return o;
-}
 
 template <int ITEMS>
 __global__ void __launch_bounds__(256) fp8_quant_rows(const u32x4* __restrict__ A, u32x2* __restrict__ Aq,

@@ -32,8 +32,10 @@ reference (Tilebench has no quantized checkpoints); their conventions are:
   are re-encoded as e4m3fn by value: every fnuz value that is a multiple of
   2^-9 is an fn value, and the eight magnitudes that are odd multiples of
   2^-10 (all below 2^-6) round to nearest even.  Block
-  scales (one per 128 x 128 tile) do not fit a row/column-scaled GEMM and are
-  rejected.
+  scales (one per 128 x 128 tile, [ceil(N/128), ceil(K/128)]: DeepSeek-V3's
+  weight_scale_inv) select the block-scaled GEMM (Fp8BlockWeights).
+* Decode slab layout: not a checkpoint format but the W4A16 decode's own
+  weight layout, converted once at load (w4a16_to_slabs below).
 """
 from __future__ import annotations
 
@@ -61,6 +63,15 @@ class Fp8Weights:
     """fp8 GEMM operands: e4m3fn codes of W^T and one fp32 scale per column."""
     wqT: torch.Tensor      # uint8 [N, K]
     sw: torch.Tensor       # fp32 [N]
+
+
+@dataclass
+class Fp8BlockWeights:
+    """Block-scaled fp8 GEMM operands (tb_fp8_block_gemm): e4m3fn codes of W^T
+    and one fp32 scale per 128 x 128 tile."""
+    wqT: torch.Tensor      # uint8 [N, K]
+    sw: torch.Tensor       # fp32 [ceil(N/128), K/128]
+    block: int = 128
 
 
 # ----------------------------------------------------------------------------- nibbles
@@ -265,10 +276,13 @@ def _fnuz_to_fn_codes(codes: torch.Tensor) -> torch.Tensor:
 
 
 def fp8_checkpoint_to_tb(weight: torch.Tensor, weight_scale: torch.Tensor | float | None = None, *,
-                         weight_scale_inv: torch.Tensor | float | None = None) -> Fp8Weights:
+                         weight_scale_inv: torch.Tensor | float | None = None) -> Fp8Weights | Fp8BlockWeights:
     """An fp8 linear layer (weight [N, K] in e4m3fn or e4m3fnuz, or its uint8
-    codes as e4m3fn) with a per-tensor or per-output-channel scale -> WqT codes
-    [N, K] and sw fp32 [N].
+    codes as e4m3fn) -> the operands of the GEMM its scale layout needs:
+    a per-tensor or per-output-channel scale gives Fp8Weights (WqT codes
+    [N, K], sw fp32 [N]) for tb_fp8_scaled_gemm; a scale per 128 x 128 tile
+    ([ceil(N/128), ceil(K/128)], DeepSeek-V3's weight_scale_inv) gives
+    Fp8BlockWeights for tb_fp8_block_gemm (K must then be a multiple of 128).
 
     Both checkpoint keys hold the dequantisation multiplier, W ~= Wq * scale:
     `weight_scale` (compressed-tensors / vLLM fp8 layers) and
@@ -286,13 +300,18 @@ def fp8_checkpoint_to_tb(weight: torch.Tensor, weight_scale: torch.Tensor | floa
         raise TypeError(f"unsupported fp8 weight dtype {weight.dtype}")
     s = weight_scale if weight_scale is not None else weight_scale_inv
     s = torch.as_tensor(s, dtype=torch.float32, device=weight.device)
+    blocks = (-(-N // 128), -(-K // 128))
+    if s.dim() == 2 and tuple(s.shape) == blocks and tuple(s.shape) != (N, 1):
+        if K % 128:
+            raise ValueError(f"block-scaled fp8 weight [{N}, {K}]: the block GEMM needs K % 128 == 0")
+        return Fp8BlockWeights(codes.contiguous(), s.contiguous())
     if s.numel() == 1:
         s = s.reshape(1).expand(N)
     elif s.numel() == N and (s.dim() == 1 or (s.dim() == 2 and s.shape[1] == 1)):
         s = s.reshape(N)
     else:
-        raise NotImplementedError(f"fp8 scale of shape {tuple(s.shape)} for a [{N}, {K}] weight: only per-tensor "
-                                  f"and per-output-channel scales fit the row/column-scaled GEMM (block scales do not)")
+        raise ValueError(f"fp8 scale of shape {tuple(s.shape)} for a [{N}, {K}] weight: expected a scalar, [N], "
+                         f"[N, 1] or 128 x 128 blocks {blocks}")
     return Fp8Weights(codes.contiguous(), s.contiguous().to(torch.float32))
 
 

@@ -48,6 +48,8 @@ SIGNATURES: dict[str, list] = {
     "tb_fused_moe_w4a16_workspace_size": [_c_i64] * 5 + [ctypes.POINTER(_c_i64)],
     "tb_fused_moe_w4a16": [_c_p] * 9 + [_c_i64] * 7 + [_c_p, _c_i64, _c_p],
     "tb_fp8_scaled_gemm": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p],
+    "tb_fp8_act_quant_blocks": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_p],
+    "tb_fp8_block_gemm": [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p],
     "tb_weight_dequant": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_int, _c_p],
     "tb_dequantize_rowwise": [_c_p, _c_p, _c_p, _c_i64, _c_i64, _c_p],
     "tb_quantize_global": [_c_p, _c_p, _c_i64, _c_p],
