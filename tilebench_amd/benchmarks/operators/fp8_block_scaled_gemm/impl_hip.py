@@ -30,7 +30,7 @@ def run(Aq: torch.Tensor, WqT: torch.Tensor, sa: torch.Tensor, sw: torch.Tensor,
     Y = torch.empty((M, N), dtype=torch.bfloat16, device=Aq.device)
     rt.call("tb_fp8_block_gemm", Aq.data_ptr(), WqT.data_ptr(), sa.data_ptr(), sw.data_ptr(), Y.data_ptr(), M, N, K,
             rt.stream_handle(Aq.device))
-    _last_config = {"kernel": "fp8_block_gemm", "BM": 256, "BN": 128, "BK": 128, "waves": 4}
+    _last_config = {"kernel": "fp8_block_gemm", "BM": 256, "BN": 256, "BK": 128, "waves": 8}
     return Y
 
 

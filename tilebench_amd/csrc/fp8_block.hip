@@ -13,18 +13,24 @@
 //                             in block order.  sw is the checkpoint's weight_scale_inv
 //                             layout, [ceil(N/128), K/128] row-major.
 //
-// GEMM structure.  One 256 x 128 output tile per 256-thread block: four
-// wavefronts, one per SIMD, each owning 128 x 64 (4 x 2 fragments of 32 x 32).
-// A K step is 128 bytes = one scale block.  Operands stream HBM -> LDS by DMA
-// (buffer_load ... lds) one step ahead into two stages, with the row swizzle
-// of the other fp8 kernels (chunk c of row r at slot c ^ ((r ^ (r >> 3)) & 7)).
-// Per step and fragment pair (i, j) two MFMAs (k 0..63 and 64..127) start from
-// zero and give P_kb; one fp32 FMA per element adds s_i * P_kb to the
-// accumulator, s_i = sa * sw of the lane's row in fragment row i (the tile's
-// 128 columns are one weight block, so sw is one value per step).  The step's
-// 256 activation scales go HBM -> LDS with the operands, permuted so that a
-// lane reads its four rows' scales with one 16-byte LDS read; the tile's
-// column of weight scales (K/128 values) is loaded once at the start.
+// GEMM structure.  One 256 x 256 output tile per 512-thread block: eight
+// wavefronts, two per SIMD, each owning 128 x 64 (4 x 2 fragments of 32 x 32;
+// 128 fp32 accumulator registers, all in VGPRs because the VALU adds into
+// them).  A K step is 128 bytes = one scale block.  Operands stream HBM -> LDS
+// by DMA (buffer_load ... lds) one step ahead into two stages, with the row
+// swizzle of the other fp8 kernels (chunk c of row r at slot
+// c ^ ((r ^ (r >> 3)) & 7)); DMAs past the last step go through empty
+// resources, so the loop has no branch.  Per step and fragment pair (i, j)
+// two MFMAs (k 0..63 and 64..127) start from zero and give P_kb (in VGPRs:
+// the file is compiled with the VGPR form of the MFMAs); one fp32 FMA per
+// element adds s_i * P_kb to the accumulator, s_i = sa * sw of the lane's row
+// in fragment row i (a wavefront's 64 columns lie in one weight block, so sw
+// is one value per step).  The FMAs of pair q - 1 are issued between the MFMAs
+// of pair q (the matrix pipe and the VALU work side by side; at most two block
+// sums are live).  The step's 256 activation scales go HBM -> LDS with the
+// operands, permuted so that a lane reads its four rows' scales with one
+// 16-byte LDS read; the tile's two columns of weight scales (K/128 values
+// each) are loaded once at the start.
 #include "tb_common.h"
 #include "fp8_codec.h"
 
@@ -37,15 +43,26 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2v __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 
-constexpr int BM = 256, BN = 128, BK = 128, WM = 128, WN = 64, WAVES = 4, THREADS = 256;
+constexpr int BM = 256, BK = 128, WM = 128, WN = 64;
 constexpr int FI = WM / 32, FJ = WN / 32;
-constexpr int A_STAGE = BM * BK, B_STAGE = BN * BK, STAGE = A_STAGE + B_STAGE;
-constexpr int A_DMA = BM / 8 / WAVES, B_DMA = BN / 8 / WAVES;  // 1 KiB DMA instructions per wave and step
-constexpr int MAX_KB = 512;                                     // K <= 65536
-constexpr size_t SA_OFF = 2 * (size_t)STAGE, SW_OFF = SA_OFF + 2 * BM * 4;
-constexpr size_t LDS_BYTES = SW_OFF + MAX_KB * 4;
-static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
-static_assert(A_DMA * WAVES * 8 == BM && B_DMA * WAVES * 8 == BN, "tile rows must split evenly over the DMA");
+constexpr int MAX_KB = 512;  // K <= 65536
+
+// Tile configuration: BN columns (128 or 256), WAVES wavefronts of WM x WN,
+// NSTAGE operand stages in LDS (the DMA runs NSTAGE - 1 steps ahead).
+template <int BN, int WAVES, int NSTAGE>
+struct Cfg {
+  static constexpr int THREADS = WAVES * 64;
+  static constexpr int A_STAGE = BM * BK, B_STAGE = BN * BK, STAGE = A_STAGE + B_STAGE;
+  static constexpr int A_DMA = BM / 8 / WAVES, B_DMA = BN / 8 / WAVES;  // 1 KiB DMAs per wave and step
+  static constexpr int SW_BLOCKS = BN / 128;                            // weight-scale blocks per tile
+  static constexpr size_t SA_OFF = NSTAGE * (size_t)STAGE;              // NSTAGE x 256 activation scales
+  static constexpr size_t DUMP_OFF = SA_OFF + NSTAGE * BM * 4;          // target of the idle waves' scale DMA
+  static constexpr size_t SW_OFF = DUMP_OFF + 256;                      // SW_BLOCKS x MAX_KB weight scales
+  static constexpr size_t LDS_BYTES = SW_OFF + (size_t)SW_BLOCKS * MAX_KB * 4;
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+  static_assert(A_DMA * WAVES * 8 == BM && B_DMA * WAVES * 8 == BN, "tile rows must split evenly over the DMA");
+  static_assert((BM / WM) * (BN / WN) == WAVES, "wave grid");
+};
 constexpr uint32_t RSRC_DW3 = 0x00020000u;
 constexpr uint32_t OOB = 0x80000000u;
 
@@ -82,6 +99,7 @@ __device__ __forceinline__ void dma4(uint32_t lds_addr, uint32_t voff, const i32
 // Tiles in groups of 8 tile rows, column-major inside a group; with the tile
 // count a multiple of 8, the blocks one XCD receives (every 8th block id) are
 // one contiguous run of tiles, so an XCD's L2 serves neighbouring tiles.
+template <int BN>
 __device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int& m0, int& n0) {
   constexpr int GROUP_M = 8;
   const int nb = tiles_m * tiles_n;
@@ -96,22 +114,27 @@ __device__ __forceinline__ void tile_of_block(int tiles_m, int tiles_n, int& m0,
   n0 = (in_group / rows) * BN;
 }
 
-__global__ void __launch_bounds__(THREADS, 1)
+template <int BN, int WAVES, int NSTAGE>
+__global__ void __launch_bounds__(WAVES * 64, 1)
     fp8_block_gemm(const uint8_t* __restrict__ Aq, const uint8_t* __restrict__ WqT, const float* __restrict__ sa,
                    const float* __restrict__ sw, uint16_t* __restrict__ Y, int M, int N, int K, int tiles_m,
                    int tiles_n) {
+  typedef Cfg<BN, WAVES, NSTAGE> C;
+  constexpr int A_STAGE = C::A_STAGE, STAGE = C::STAGE, A_DMA = C::A_DMA, B_DMA = C::B_DMA;
+  constexpr size_t SA_OFF = C::SA_OFF, SW_OFF = C::SW_OFF;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   int m0, n0;
-  tile_of_block(tiles_m, tiles_n, m0, n0);
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  tile_of_block<BN>(tiles_m, tiles_n, m0, n0);
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: LDS and DMA bases stay scalar
+  const int wm = wave / (BN / WN), wn = wave % (BN / WN);
   const int nkb = K / BK;
 
   const i32x4 ra = make_rsrc4(Aq, (uint32_t)M * (uint32_t)K);
   const i32x4 rb = make_rsrc4(WqT, (uint32_t)N * (uint32_t)K);
   const i32x4 rsa = make_rsrc4(sa, (uint32_t)nkb * (uint32_t)M * 4u);
-  const int nb = n0 / BN;  // this tile's weight-scale block row (BN = 128)
-  const i32x4 rsw = make_rsrc4(sw, (uint32_t)((N + 127) / 128) * (uint32_t)nkb * 4u);
+  const int nbN = (N + 127) / 128;  // weight-scale block rows
+  const i32x4 rsw = make_rsrc4(sw, (uint32_t)nbN * (uint32_t)nkb * 4u);
   uint32_t a_off[A_DMA], b_off[B_DMA];
   {
     const int lr = lane >> 3;
@@ -132,28 +155,45 @@ __global__ void __launch_bounds__(THREADS, 1)
   // of tile row 128 (p / 128) + 32 (p % 4) + (p % 128) / 4, so that the lane
   // (wm, c = lane % 32) finds its rows wm*128 + 32 i + c (i = 0..3) at
   // 128 wm + 4 c + i: one 16-byte read.
+  // Waves 4 and up have no scales to load; they issue the same DMA through an
+  // empty resource into a dump area, so every wave counts the same DMAs.
   uint32_t sa_off;
   {
     const int p = wave * 64 + lane;
     const int row = (p >> 7) * 128 + 32 * (p & 3) + ((p & 127) >> 2);
-    sa_off = m0 + row < M ? (uint32_t)(m0 + row) * 4u : OOB;
+    sa_off = wave < 4 && m0 + row < M ? (uint32_t)(m0 + row) * 4u : OOB;
   }
   const uint32_t lds0 = (uint32_t)__builtin_amdgcn_readfirstlane(
       (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
+  // DMAs of a step past the last one go through resources of size 0: they
+  // read nothing and fill a stage no step reads, so every step issues the same
+  // DMAs and waits the same way (no branch in the loop).
+  const i32x4 ra0 = make_rsrc4(Aq, 0u), rb0 = make_rsrc4(WqT, 0u), rsa0 = make_rsrc4(sa, 0u);
   auto issue = [&](int kt) {
-    const uint32_t st = lds0 + (uint32_t)((kt & 1) * STAGE);
-    const uint32_t soff = (uint32_t)(kt * BK);
+    const int sidx = kt % NSTAGE;
+    const bool live = kt < nkb;
+    const uint32_t st = lds0 + (uint32_t)(sidx * STAGE);
+    const uint32_t soff = live ? (uint32_t)(kt * BK) : 0u;
 #pragma unroll
-    for (int i = 0; i < A_DMA; ++i) dma16(st + (uint32_t)((wave * A_DMA + i) * 1024), a_off[i], ra, soff);
+    for (int i = 0; i < A_DMA; ++i)
+      dma16(st + (uint32_t)((wave * A_DMA + i) * 1024), a_off[i], live ? ra : ra0, soff);
 #pragma unroll
-    for (int i = 0; i < B_DMA; ++i) dma16(st + A_STAGE + (uint32_t)((wave * B_DMA + i) * 1024), b_off[i], rb, soff);
-    dma4(lds0 + (uint32_t)(SA_OFF + (kt & 1) * BM * 4 + wave * 256), sa_off, rsa, (uint32_t)kt * (uint32_t)M * 4u);
+    for (int i = 0; i < B_DMA; ++i)
+      dma16(st + A_STAGE + (uint32_t)((wave * B_DMA + i) * 1024), b_off[i], live ? rb : rb0, soff);
+    const bool scales = wave < 4;
+    dma4(lds0 + (uint32_t)(scales ? SA_OFF + sidx * BM * 4 + wave * 256 : C::DUMP_OFF), sa_off,
+         live && scales ? rsa : rsa0, live ? (uint32_t)kt * (uint32_t)M * 4u : 0u);
   };
-  // The tile's weight scales sw[nb, 0 .. nkb-1]: wave w loads entries 64 q + lane for q = w, w + 4, ...
-  for (int q = wave; q * 64 < nkb; q += WAVES) {
-    const int kb = q * 64 + lane;
-    dma4(lds0 + (uint32_t)(SW_OFF + q * 256), kb < nkb ? (uint32_t)kb * 4u : OOB, rsw,
-         (uint32_t)nb * (uint32_t)nkb * 4u);
+  constexpr int DMA_PER_STEP = A_DMA + B_DMA + 1;  // per wavefront
+  // The tile's weight scales sw[n0 / 128 + b, 0 .. nkb-1] (b < BN / 128) at
+  // LDS float b * MAX_KB + kb: instruction q = b * nq + c loads kb = 64 c + lane.
+  {
+    const int nq = (nkb + 63) / 64;
+    for (int q = wave; q < C::SW_BLOCKS * nq; q += WAVES) {
+      const int b = q / nq, kb = (q % nq) * 64 + lane, nb = n0 / 128 + b;
+      dma4(lds0 + (uint32_t)(SW_OFF + b * MAX_KB * 4 + (q % nq) * 256),
+           kb < nkb && nb < nbN ? ((uint32_t)nb * (uint32_t)nkb + (uint32_t)kb) * 4u : OOB, rsw, 0u);
+    }
   }
 
   const int a_row = wm * WM + (lane & 31);
@@ -173,45 +213,101 @@ __global__ void __launch_bounds__(THREADS, 1)
     for (int j = 0; j < FJ; ++j) acc[i][j] = f32x16{};
 
   constexpr int WAIT_VM0 = 0 | (7 << 4) | (15 << 8);
-  const float* lsw = reinterpret_cast<const float*>(lds + SW_OFF);
-  issue(0);
-  __builtin_amdgcn_s_waitcnt(WAIT_VM0);
+  constexpr int WAIT_VM_STEP = DMA_PER_STEP | (7 << 4) | (15 << 8);  // all but the last step's DMAs landed
+  static_assert(DMA_PER_STEP < 16, "vmcnt immediate");
+  const float* lsw = reinterpret_cast<const float*>(lds + SW_OFF) + (wn * WN / 128) * MAX_KB;
+#pragma unroll
+  for (int k = 0; k < NSTAGE - 1; ++k) issue(k);
+  if constexpr (NSTAGE > 2)
+    __builtin_amdgcn_s_waitcnt(WAIT_VM_STEP);
+  else
+    __builtin_amdgcn_s_waitcnt(WAIT_VM0);
   __syncthreads();
+  // Software pipeline over fragment pairs: the MFMAs of pair q run while the
+  // VALU adds pair q - 1's scaled block sum into its accumulator; the last
+  // pair of a step is added at the start of the next step, under the latency
+  // of that step's first fragment reads.  A-fragments of row i + 1 are read
+  // while row i's pairs run (two buffers), B-fragments once per step.
+  f32x16 plast = f32x16{};
+  float slast = 0.f;
   for (int kt = 0; kt < nkb; ++kt) {
-    const bool more = kt + 1 < nkb;
-    if (more) issue(kt + 1);
-    const uint8_t* sa_ = lds + (kt & 1) * STAGE;
+    // stage (kt + NSTAGE - 1) % NSTAGE was last read in step kt - 1, before the barrier that ended it
+    issue(kt + NSTAGE - 1);
+    const int sidx = kt % NSTAGE;
+    const uint8_t* sa_ = lds + sidx * STAGE;
     const uint8_t* sb_ = sa_ + A_STAGE;
-    i32x8 fa0[FI], fa1[FI], fb0[FJ], fb1[FJ];
+    // A fragments: two buffers (row i + 1 read while row i runs) with one wave
+    // per SIMD; one buffer (row i + 1 read after row i's last MFMA) with two,
+    // whose registers are half as many and whose other wave covers the wait.
+    constexpr int FAB = WAVES > 4 ? 1 : 2;
+    i32x8 fb0[FJ], fb1[FJ], fa0[FAB], fa1[FAB];
 #pragma unroll
     for (int j = 0; j < FJ; ++j) {
       fb0[j] = frag(sb_, b_row + j * 32, 0);
       fb1[j] = frag(sb_, b_row + j * 32, 1);
     }
-#pragma unroll
-    for (int i = 0; i < FI; ++i) {
-      fa0[i] = frag(sa_, a_row + i * 32, 0);
-      fa1[i] = frag(sa_, a_row + i * 32, 1);
-    }
-    const f32x4 sav = *reinterpret_cast<const f32x4*>(lds + SA_OFF + (kt & 1) * BM * 4 + (wm * 128 + 4 * (lane & 31)) * 4);
+    fa0[0] = frag(sa_, a_row, 0);
+    fa1[0] = frag(sa_, a_row, 1);
+    const f32x4 sav = *reinterpret_cast<const f32x4*>(lds + SA_OFF + sidx * BM * 4 + (wm * 128 + 4 * (lane & 31)) * 4);
     const float swv = lsw[kt];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[FI - 1][FJ - 1][e] = __builtin_fmaf(plast[e], slast, acc[FI - 1][FJ - 1][e]);
     float s[FI];
 #pragma unroll
     for (int i = 0; i < FI; ++i) s[i] = sav[i] * swv;
+    f32x16 pprev = f32x16{};
 #pragma unroll
-    for (int i = 0; i < FI; ++i)
+    for (int i = 0; i < FI; ++i) {
+      if (FAB == 2 && i + 1 < FI) {
+        fa0[(i + 1) % FAB] = frag(sa_, a_row + (i + 1) * 32, 0);
+        fa1[(i + 1) % FAB] = frag(sa_, a_row + (i + 1) * 32, 1);
+      }
 #pragma unroll
       for (int j = 0; j < FJ; ++j) {
         // transposed product (W^T fragment first): a lane holds 4 consecutive columns
-        f32x16 p = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb0[j], fa0[i], f32x16{}, 0, 0, 0, 0, 0, 0);
-        p = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb1[j], fa1[i], p, 0, 0, 0, 0, 0, 0);
+        f32x16 p = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb0[j], fa0[i % FAB], f32x16{}, 0, 0, 0, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb1[j], fa1[i % FAB], p, 0, 0, 0, 0, 0, 0);
+        const int q = i * FJ + j;
+        if (q > 0) {
+          const int pi = (q - 1) / FJ, pj = (q - 1) % FJ;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[i][j][e] = __builtin_fmaf(p[e], s[i], acc[i][j][e]);
+          for (int e = 0; e < 16; ++e) acc[pi][pj][e] = __builtin_fmaf(pprev[e], s[pi], acc[pi][pj][e]);
+        }
+        pprev = p;
       }
+      if (FAB == 1 && i + 1 < FI) {
+        fa0[0] = frag(sa_, a_row + (i + 1) * 32, 0);
+        fa1[0] = frag(sa_, a_row + (i + 1) * 32, 1);
+      }
+    }
+    // Issue order of the step (one scheduling region): pair q's two MFMAs with
+    // pair q - 1's 16 FMAs between and after them (the matrix pipe runs pair q
+    // while the VALU adds pair q - 1), and the next A row's fragment reads
+    // (4 LDS reads) beside the first MFMA of each row.  At most two block sums
+    // are live at a time.
+#pragma unroll
+    for (int q = 0; q < FI * FJ; ++q) {
+      const bool next_row = q / FJ + 1 < FI;
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                      // MFMA, first k half
+      if (FAB == 2 && q % FJ == 0 && next_row) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // next row's reads
+      if (q > 0) __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);          // FMAs of pair q - 1
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                      // MFMA, second k half
+      if (FAB == 1 && q % FJ == FJ - 1 && next_row) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      if (q > 0) __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+    }
+    plast = pprev;
+    slast = s[FI - 1];
     // stage kt + 1 must land before the barrier that hands it to the next step
-    if (more) __builtin_amdgcn_s_waitcnt(WAIT_VM0);
+    // (with three stages the DMAs of step kt + 2, issued after it, may still be in flight)
+    if constexpr (NSTAGE > 2)
+      __builtin_amdgcn_s_waitcnt(WAIT_VM_STEP);
+    else
+      __builtin_amdgcn_s_waitcnt(WAIT_VM0);
     __syncthreads();
   }
+  __builtin_amdgcn_s_waitcnt(WAIT_VM0);  // the DMAs issued past the end
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[FI - 1][FJ - 1][e] = __builtin_fmaf(plast[e], slast, acc[FI - 1][FJ - 1][e]);
 
   // Epilogue straight from registers: elements 4g .. 4g+3 of fragment (i, j)
   // are row i*32 + lane%32, columns j*32 + g*8 + (lane/32)*4 + 0..3 of the wave
@@ -270,8 +366,30 @@ __global__ void __launch_bounds__(256) fp8_quant_blocks(const u32x4* __restrict_
   Aq[blk * 16 + sub] = quantize_chunk(x, s, y, m);
 }
 
+template <int BN, int WAVES, int NSTAGE>
+tb_status launch_block(const uint8_t* Aq, const uint8_t* WqT, const float* sa, const float* sw, uint16_t* Y,
+                       int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  typedef Cfg<BN, WAVES, NSTAGE> C;
+  auto kern = &fp8_block_gemm<BN, WAVES, NSTAGE>;
+  if (tb_status st = tb::reserve_lds(reinterpret_cast<const void*>(kern), C::LDS_BYTES, "tb_fp8_block_gemm"))
+    return st;
+  const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
+  hipLaunchKernelGGL(kern, dim3(tiles_m * tiles_n), dim3(C::THREADS), C::LDS_BYTES, stream, Aq, WqT, sa, sw, Y, (int)M,
+                     (int)N, (int)K, tiles_m, tiles_n);
+  return tb::launch_status("tb_fp8_block_gemm");
+}
+
 }  // namespace fp8blk
 }  // namespace tb
+
+// The launched configuration: 256 x 256 tiles on eight wavefronts (two per
+// SIMD), two stages.  Measured at 8192^3 (same box, bit-identical outputs):
+// 256 x 128 on four wavefronts with three stages 722 us, this 561-568 us.
+#ifndef FP8BLK_BN
+#define FP8BLK_BN 256
+#define FP8BLK_WAVES 8
+#define FP8BLK_NSTAGE 2
+#endif
 
 extern "C" tb_status tb_fp8_act_quant_blocks(const uint16_t* A, uint8_t* Aq, float* sa, int64_t M, int64_t K,
                                              hipStream_t stream) {
@@ -305,10 +423,5 @@ extern "C" tb_status tb_fp8_block_gemm(const uint8_t* Aq, const uint8_t* WqT, co
   TB_CHECK_ALIGN(sa, 4, "sa");
   TB_CHECK_ALIGN(sw, 4, "sw");
   TB_CHECK_ALIGN(Y, 8, "Y");
-  if (tb_status st = tb::reserve_lds(reinterpret_cast<const void*>(&fp8_block_gemm), LDS_BYTES, "tb_fp8_block_gemm"))
-    return st;
-  const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
-  hipLaunchKernelGGL(fp8_block_gemm, dim3(tiles_m * tiles_n), dim3(THREADS), LDS_BYTES, stream, Aq, WqT, sa, sw, Y,
-                     (int)M, (int)N, (int)K, tiles_m, tiles_n);
-  return tb::launch_status("tb_fp8_block_gemm");
+  return launch_block<FP8BLK_BN, FP8BLK_WAVES, FP8BLK_NSTAGE>(Aq, WqT, sa, sw, Y, M, N, K, stream);
 }
