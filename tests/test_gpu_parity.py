@@ -178,7 +178,8 @@ def test_gating_filter_half_dtypes(gpu, E, dt):
     _say("gating filter", E, dt)
     tdt = torch.float16 if dt == "fp16" else torch.bfloat16
     logits, M, E, k = T.generate_moe_topk_gating_inputs(4099, E, 8, dtype=tdt, seed=E, device="cpu")
-    logits[40:48] = torch.from_numpy(_filter_rows(E)).to(tdt)
+    special = torch.from_numpy(_filter_rows(E)).to(tdt)
+    logits[40:40 + special.shape[0]] = special
     w, i = impl_hip.run(logits.to(gpu), M, E, k)
     torch.cuda.synchronize()
     bits = logits.view(torch.int16).numpy().view(np.uint16) if dt == "bf16" else logits.numpy()
