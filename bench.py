@@ -197,6 +197,24 @@ def _slab_repack_us():
     return {"repack_us": round(e0.elapsed_time(e1) * 100.0, 2)}
 
 
+def _w_fp8_quant_blocks():
+    from tilebench_amd.data import tensors as T
+    from tilebench_amd.benchmarks.operators.fp8_act_quant_blocks import impl_hip, impl_torch
+
+    M = K = 8192
+    nbytes = 2 * M * K + M * K + 4 * M * (K // 128)
+
+    def cpu():
+        x = T.generate_fp8_act_quant_blocks_inputs(M, K, seed=2, device="cpu")
+        return (lambda: impl_torch.run(*x)), nbytes, "full 8192 x 8192"
+
+    return dict(name="fp8_act_quant_blocks", config={"workload": "fp8_act_quant_blocks", "M": M, "K": K, "block": 128},
+                metric="fp8 per-token 128-channel quant HBM throughput", unit="GB/s", dtype="fp16->e4m3",
+                bound="hbm", bytes=nbytes, flops=None, out_bytes=M * K + 4 * M * (K // 128),
+                inputs=lambda: T.generate_fp8_act_quant_blocks_inputs(M, K, seed=2, device="cuda"),
+                step=lambda x: impl_hip.run(*x), kernel="tb::fp8blk::fp8_quant_blocks", cpu=cpu)
+
+
 def _w_fp8_gemm():
     from tilebench_amd.data import tensors as T
     from tilebench_amd.benchmarks.operators.fp8_scaled_gemm import impl_hip, impl_torch
@@ -239,7 +257,7 @@ def _w_fp8_block_gemm():
                 unit="TFLOP/s", dtype="e4m3 x e4m3 -> bf16 (fp32 acc)", bound="mfma", peak_key="fp8", bytes=nbytes,
                 flops=flops, out_bytes=2 * M * N,
                 inputs=lambda: T.generate_fp8_block_scaled_gemm_inputs(M, N, K, seed=2, device="cuda"),
-                step=lambda x: impl_hip.run(*x), kernel="tb::fp8blk::fp8_block_gemm", cpu=cpu)
+                step=lambda x: impl_hip.run(*x), kernel="tb::fp8blk::fp8_block_gemm<256, 8, 2>", cpu=cpu)
 
 
 def _w_grouped():
@@ -435,6 +453,7 @@ WORKLOADS = {
     "fp8_act_quant": _w_fp8_quant,
     "fp8_scaled_gemm": _w_fp8_gemm,
     "fp8_block_scaled_gemm": _w_fp8_block_gemm,
+    "fp8_act_quant_blocks": _w_fp8_quant_blocks,
     "moe_w4a16_grouped_gemm": _w_grouped,
     "fused_moe_w4a16": _w_fused_moe,
     "weight_dequant": _w_weight_dequant,

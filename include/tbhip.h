@@ -261,7 +261,7 @@ tb_status tb_fp8_scaled_gemm(const uint8_t* Aq, const uint8_t* WqT, const float*
  *   the block sums in fp32 on the e4m3 matrix cores, scaled and added in fp32
  *   in block order, one RNE rounding.  WqT uint8 [N, K]; sw fp32
  *   [ceil(N/128), K/128] row-major.  Requires K % 128 == 0, K <= 65536,
- *   N % 8 == 0, each operand < 2 GiB, Aq / WqT 16-byte and Y 8-byte aligned.
+ *   N % 8 == 0, each operand < 2 GiB, Aq, WqT and Y 16-byte aligned.
  * Replace: the reference's block-scaled weight dequantisation
  *   (weight_dequant/impl_torch.py:4-8, X * S[i//T, j//T] with T = 128) fused
  *   into its fp8 GEMM (matmul_fp32_fp16_fp8/impl_triton.py:124 run(a, b)).

@@ -213,3 +213,29 @@ def test_filter_regex_under_the_cxx_regex_grammar(tmp_path):
         out = subprocess.run([str(exe), rgx, grammar], input="\n".join(names) + "\n", capture_output=True,
                              text=True, check=True).stdout.split()
         assert out == ["1", "1", "1", "0", "0", "0", "0", "0", "1", "1", "0", "0"], grammar
+
+
+def test_counter_summary_merges_passes_and_scales_traffic(tmp_path):
+    """Counters from two passes of one kernel average over the dispatches that
+    report each counter; traffic scales FETCH/WRITE so the copy probe reads its
+    known 512 MiB."""
+    from tilebench_amd.profiling import counters as pc
+
+    hdr = '"Dispatch_Id","Grid_Size","Kernel_Name","Counter_Name","Counter_Value"\n'
+
+    def write(d, rows):
+        d.mkdir()
+        (d / "run_counter_collection.csv").write_text(hdr + "".join(
+            f'{i},{33554432 if "copy" in k else 256},"{k}","{c}",{v}\n' for i, k, c, v in rows))
+
+    write(tmp_path / "a", [(1, "tb::k(int)", "SQ_WAVES", 10), (2, "tb::k(int)", "SQ_WAVES", 30),
+                           (1, "tb::k(int)", "GRBM_GUI_ACTIVE", 800), (2, "tb::k(int)", "GRBM_GUI_ACTIVE", 800)])
+    write(tmp_path / "b", [(7, "tb::k(int)", "SQ_VALU_MFMA_BUSY_CYCLES", 512)])
+    r = pc.per_dispatch([str(tmp_path / "a"), str(tmp_path / "b")])["tb::k"]
+    assert r["dispatches"] == 2
+    assert r["counters"] == {"GRBM_GUI_ACTIVE": 800, "SQ_VALU_MFMA_BUSY_CYCLES": 512, "SQ_WAVES": 20}
+    assert abs(pc.derived(r["counters"])["mfma_utilisation"] - 512 / (100 * 1024)) < 1e-12
+    write(tmp_path / "f", [(1, "tb::copy_kernel(char*)", "FETCH_SIZE", 262144), (2, "tb::x(int)", "FETCH_SIZE", 100)])
+    write(tmp_path / "w", [(1, "tb::copy_kernel(char*)", "WRITE_SIZE", 524288), (2, "tb::x(int)", "WRITE_SIZE", 10)])
+    t = pc.traffic(str(tmp_path / "f"), str(tmp_path / "w"))
+    assert t == {"tb::x": {"fetch_bytes": 204800, "write_bytes": 10240, "fetch_factor": 2.0, "write_factor": 1.0}}

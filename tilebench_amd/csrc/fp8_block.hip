@@ -309,27 +309,39 @@ __global__ void __launch_bounds__(WAVES * 64, 1)
 #pragma unroll
   for (int e = 0; e < 16; ++e) acc[FI - 1][FJ - 1][e] = __builtin_fmaf(plast[e], slast, acc[FI - 1][FJ - 1][e]);
 
-  // Epilogue straight from registers: elements 4g .. 4g+3 of fragment (i, j)
-  // are row i*32 + lane%32, columns j*32 + g*8 + (lane/32)*4 + 0..3 of the wave
-  // tile (N % 8 == 0: four columns are all in or all out).  One RNE rounding
-  // to bf16 by the hardware converter.
+  // Epilogue: element 4g + e of fragment (i, j) is row i*32 + lane%32, column
+  // j*32 + g*8 + (lane/32)*4 + e of the wave tile.  One RNE rounding to bf16 by
+  // the hardware converter; the tile is staged in LDS (the operand stages are
+  // free now) and stored as 16-byte row chunks, so every HBM write covers whole
+  // lines (stored straight from the registers, 8 bytes per lane, the writes
+  // counted 2x the output's bytes).
+  constexpr int C_STRIDE = BN + 8;  // bf16 per staged row (16-byte pad)
+  static_assert((size_t)BM * C_STRIDE * 2 <= C::LDS_BYTES, "staged output tile fits in LDS");
+  __syncthreads();  // every wave is done with the operand stages
+  uint16_t* ct = reinterpret_cast<uint16_t*>(lds);
 #pragma unroll
-  for (int i = 0; i < FI; ++i) {
-    const int m = m0 + a_row + i * 32;
-    if (m >= M) continue;
+  for (int i = 0; i < FI; ++i)
 #pragma unroll
     for (int j = 0; j < FJ; ++j)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int n = n0 + wn * WN + j * 32 + g * 8 + (lane >> 5) * 4;
-        if (n >= N) continue;
+        const int row = a_row + i * 32;
+        const int col = wn * WN + j * 32 + g * 8 + (lane >> 5) * 4;
         u32x2 v;
         v[0] = __builtin_bit_cast(uint32_t, __builtin_convertvector(
                                                 (f32x2v{acc[i][j][4 * g], acc[i][j][4 * g + 1]}), bf16x2v));
         v[1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(
                                                 (f32x2v{acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]}), bf16x2v));
-        *reinterpret_cast<u32x2*>(Y + (int64_t)m * N + n) = v;
+        *reinterpret_cast<u32x2*>(ct + row * C_STRIDE + col) = v;
       }
+  __syncthreads();
+  const int rows = min(BM, M - m0), cols = min(BN, N - n0);
+  for (int idx = t; idx < BM * (BN / 8); idx += C::THREADS) {
+    const int row = idx / (BN / 8), ch = idx % (BN / 8);
+    if (row < rows && ch * 8 < cols) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(ct + row * C_STRIDE + ch * 8);
+      *reinterpret_cast<u32x4*>(Y + (int64_t)(m0 + row) * N + n0 + ch * 8) = v;
+    }
   }
 }
 
@@ -422,6 +434,6 @@ extern "C" tb_status tb_fp8_block_gemm(const uint8_t* Aq, const uint8_t* WqT, co
   TB_CHECK_ALIGN(WqT, 16, "WqT");
   TB_CHECK_ALIGN(sa, 4, "sa");
   TB_CHECK_ALIGN(sw, 4, "sw");
-  TB_CHECK_ALIGN(Y, 8, "Y");
+  TB_CHECK_ALIGN(Y, 16, "Y");
   return launch_block<FP8BLK_BN, FP8BLK_WAVES, FP8BLK_NSTAGE>(Aq, WqT, sa, sw, Y, M, N, K, stream);
 }
