@@ -363,6 +363,18 @@ tb_status tb_probe_read(const void* src, int64_t bytes, uint32_t key, uint32_t* 
  */
 tb_status tb_probe_mfma(int kind, int64_t blocks, int64_t iters, float* out, hipStream_t stream);
 
+/*
+ * Clock probe: `blocks` x 256 threads running the fp16 loop of tb_probe_mfma
+ * (kind 0) between two reads of the shader clock counter and of the constant
+ * 100 MHz counter; block b writes the two differences to clocks[2b] and
+ * clocks[2b + 1] (its average shader clock is 100 MHz x their ratio) and one
+ * float per wavefront to sink[4 * blocks].  Shows how the clock under an
+ * MFMA-bound load depends on what ran before (tilebench_amd.profiling.clock).
+ * No counterpart in the reference: a probe of this backend's measurement
+ * conditions, beside the calibration probes above.
+ */
+tb_status tb_probe_clock(int64_t blocks, int64_t iters, uint64_t* clocks, float* sink, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

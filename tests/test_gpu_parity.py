@@ -695,7 +695,10 @@ def test_grouped_gemm_segments_equal_dense_kernel(gpu):
     Ad, pd, sd, zd = A.to(gpu), p.to(gpu), s.to(gpu), z.to(gpu)
     Y = gg.run(Ad, pd, sd, zd, off.to(gpu), G)
     o = off.tolist()
-    for e in (0, 3, 15):
+    last = {(o[e + 1] - o[e]) % 256 for e in range(16) if o[e + 1] - o[e] > 16}
+    # both last-tile shapes run: 256 rows (remainder 0) and 128 rows (remainder 128)
+    assert {0, 128} <= last, last
+    for e in range(16):
         lo, hi = o[e], o[e + 1]
         if hi - lo > 16:
             Ye = wg.run(Ad[lo:hi], pd[e], sd[e], zd[e], G)

@@ -239,3 +239,71 @@ def test_counter_summary_merges_passes_and_scales_traffic(tmp_path):
     write(tmp_path / "w", [(1, "tb::copy_kernel(char*)", "WRITE_SIZE", 524288), (2, "tb::x(int)", "WRITE_SIZE", 10)])
     t = pc.traffic(str(tmp_path / "f"), str(tmp_path / "w"))
     assert t == {"tb::x": {"fetch_bytes": 204800, "write_bytes": 10240, "fetch_factor": 2.0, "write_factor": 1.0}}
+
+
+def test_suite_trace_splits_workloads_at_fill_blocks(tmp_path):
+    """Each workload's segment starts at a block of fill launches; the timed
+    average is over the last `steps` launches of its roofline kernel there."""
+    import json
+
+    from tilebench_amd.profiling import suite_trace as st
+
+    fill = "void at::native::vectorized_elementwise_kernel<4, at::native::FillFunctor<long>, at::detail::Array<char*, 1> >(int, at::native::FillFunctor<long>, at::detail::Array<char*, 1>)"
+    seq = [(fill, 1), (fill, 1), ("tb::a(int)", 5), ("tb::a(int)", 7), ("tb::a(int)", 9),
+           (fill, 1), ("tb::b(int)", 100), ("tb::a(int)", 1000), ("tb::b(int)", 300), ("tb::b(int)", 500)]
+    t, rows = 0, []
+    for name, dur in seq:
+        rows.append(f'"{name}",{t},{t + dur}\n')
+        t += dur + 10
+    (tmp_path / "bench_kernel_trace.csv").write_text('"Kernel_Name","Start_Timestamp","End_Timestamp"\n' + "".join(rows))
+    (tmp_path / "bench_kernel_stats.csv").write_text('"Name","Calls","AverageNs","MinNs","MaxNs"\n'
+                                                     '"tb::a(int)",4,255.25,5,1000\n')
+    line = {"steps": 2, "config": {"workload": "wa"}, "roofline": {"kernel": "tb::a"}, "ms_per_step": 0.008,
+            "suite": {"wb": {"kernel": "tb::b", "ms": 0.4}}}
+    (tmp_path / "bench.json").write_text("[bench] wb: 400 us/step\n" + json.dumps(line) + "\n")
+    out = st.summarize(str(tmp_path), str(tmp_path / "bench.json")).splitlines()
+    assert out[1].split() == ["wa", "(headline)", "tb::a", "3", "0.01", "8.00"]
+    assert out[2].split() == ["wb", "tb::b", "3", "0.40", "400.00"]
+    assert out[-1].split() == ["tb::a", "4", "0.26", "0.01", "1.00"]
+    with pytest.raises(ValueError, match="fill blocks"):
+        line["suite"]["wc"] = {"kernel": "tb::c", "ms": 1.0}
+        (tmp_path / "bench.json").write_text(json.dumps(line) + "\n")
+        st.summarize(str(tmp_path), str(tmp_path / "bench.json"))
+
+
+def test_traffic_table_averages_each_workloads_own_dispatches(tmp_path):
+    """The counter passes split into workloads at the fill blocks; a kernel shared by
+    two workloads is averaged per workload, and the copy probe sets the scale."""
+    import json
+
+    from tilebench_amd.profiling import counters as pc
+
+    fill = "void at::native::vectorized_elementwise_kernel<4, at::native::FillFunctor<long>, at::detail::Array<char*, 1> >(int, at::native::FillFunctor<long>, at::detail::Array<char*, 1>)"
+    seq = [(fill, 1), ("tb::d(int)", 10), ("tb::d(int)", 30), (fill, 1), ("tb::d(int)", 100),
+           (fill, 1), ("tb::copy_kernel(char*)", 0)]
+    for counter, copy_kib in (("FETCH_SIZE", 262144), ("WRITE_SIZE", 524288)):
+        d = tmp_path / counter
+        d.mkdir()
+        rows = "".join(f'{i + 1},{33554432 if "copy" in k else 64},"{k}","{counter}",{copy_kib if "copy" in k else v}\n'
+                       for i, (k, v) in enumerate(seq))
+        (d / "bench_counter_collection.csv").write_text(
+            '"Dispatch_Id","Grid_Size","Kernel_Name","Counter_Name","Counter_Value"\n' + rows)
+    line = {"steps": 1, "config": {"workload": "a"}, "ms_per_step": 1.0,
+            "roofline": {"kernel": "tb::d", "alg_read_bytes": 10240, "alg_write_bytes": 1024},
+            "suite": {"b": {"kernel": "tb::d", "ms": 1.0, "alg_read_bytes": 51200, "alg_write_bytes": 2048},
+                      "copy": {"kernel": "tb::copy_kernel", "ms": 1.0}}}
+    (tmp_path / "bench.json").write_text(json.dumps(line) + "\n")
+    rows = pc.workload_table(str(tmp_path / "FETCH_SIZE"), str(tmp_path / "WRITE_SIZE"), str(tmp_path / "bench.json"))
+    assert [(r["workload"], r["dispatches"]) for r in rows] == [("a (headline)", 2), ("b", 1), ("copy", 1)]
+    assert rows[0]["fetch_bytes"] == 20 * 1024 * 2.0 and rows[0]["write_bytes"] == 20 * 1024
+    assert rows[1]["fetch_bytes"] == 100 * 1024 * 2.0
+    text = pc.format_table(rows).splitlines()
+    assert text[1].split()[-6:] == ["40", "10", "4.00", "20", "1", "20.00"]
+
+
+def test_clock_probe_needs_a_gpu(monkeypatch, capsys):
+    import torch
+    from tilebench_amd.profiling import clock
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    assert clock.main(["--operator", ""]) == 2
+    assert "needs a GPU" in capsys.readouterr().err

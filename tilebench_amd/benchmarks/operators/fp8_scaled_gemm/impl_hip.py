@@ -29,7 +29,7 @@ def run(Aq: torch.Tensor, Wq: torch.Tensor, sa: torch.Tensor, sw: torch.Tensor, 
     Y = torch.empty((M, N), dtype=torch.bfloat16, device=Aq.device)
     rt.call("tb_fp8_scaled_gemm", Aq.data_ptr(), WqT.data_ptr(), sa.data_ptr(), sw.data_ptr(), Y.data_ptr(), M, N, K,
             rt.stream_handle(Aq.device))
-    _last_config = {"kernel": "fp8_gemm_kernel", "BM": 256, "BN": 256, "BK": 128, "waves": 8}
+    _last_config = {"kernel": "fp8_gemm_kernel", "BM": 256, "BN": 256, "BK": 128, "waves": 4}
     return Y
 
 

@@ -27,7 +27,8 @@ def run(A: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, zeros: torc
     Y = torch.empty((R, N), dtype=torch.float16, device=A.device)
     rt.call("tb_moe_w4a16_grouped_gemm", A.data_ptr(), packed.data_ptr(), scales.data_ptr(), zeros.data_ptr(),
             offsets.data_ptr(), Y.data_ptr(), R, E, N, K, group, rt.stream_handle(A.device))
-    _last_config = {"kernel": "w4a16_grouped", "BM": 256, "BN": 256, "BK": 64, "waves": 8}
+    _last_config = {"kernel": "w4a16_grouped", "BM": 256, "BN": 256, "BK": 64, "waves": 4,
+                    "last_tiles": "256 x 128 for <= 128 columns"}
     return Y
 
 

@@ -156,6 +156,44 @@ __global__ void __launch_bounds__(256) mfma_probe_kernel(float* __restrict__ out
   out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
+// Clock probe: the fp16 loop of mfma_probe_kernel<0> between two reads of the
+// shader clock counter (s_memtime) and of the constant 100 MHz counter
+// (s_memrealtime).  Thread 0 of block b writes both differences to
+// clocks[2 b] and clocks[2 b + 1], so the host reads the block's average
+// shader clock as 100 MHz x the ratio; every wavefront's first lane writes a
+// sum of its accumulators to sink[4 b + wave] (so no MFMA is dead code).
+__global__ void __launch_bounds__(256) clock_probe_kernel(unsigned long long* __restrict__ clocks,
+                                                          float* __restrict__ sink, int iters, float seed) {
+  const uint64_t c0 = __builtin_amdgcn_s_memtime();
+  const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
+  f32x16 acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = f32x16{};
+  const int lane = threadIdx.x;
+  h8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = (_Float16)(seed * (lane + i));
+    b[i] = (_Float16)(seed * (lane - i));
+  }
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[i], 0, 0, 0);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s += acc[i][e];
+  const uint64_t c1 = __builtin_amdgcn_s_memtime();
+  const uint64_t r1 = __builtin_amdgcn_s_memrealtime();
+  if ((threadIdx.x & 63) == 0) sink[(int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)] = s;
+  if (threadIdx.x == 0) {
+    clocks[2 * (int64_t)blockIdx.x] = c1 - c0;
+    clocks[2 * (int64_t)blockIdx.x + 1] = r1 - r0;
+  }
+}
+
 static unsigned grid_for(int64_t n16) { return (unsigned)((n16 + 255) / 256); }
 
 }  // namespace tb
@@ -190,6 +228,15 @@ tb_status tb_probe_mfma(int kind, int64_t blocks, int64_t iters, float* out, hip
   else
     hipLaunchKernelGGL(tb::mfma_probe_kernel<3>, grid, block, 0, stream, out, (int)iters, 1e-3f);
   return tb::launch_status("tb_probe_mfma");
+}
+
+tb_status tb_probe_clock(int64_t blocks, int64_t iters, uint64_t* clocks, float* sink, hipStream_t stream) {
+  TB_CHECK_ARG(clocks && sink && blocks > 0 && blocks < (1ll << 31) && iters > 0 && iters < (1ll << 31),
+               "tb_probe_clock: bad arguments");
+  TB_CHECK_ALIGN(clocks, 8, "clocks");
+  hipLaunchKernelGGL(tb::clock_probe_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     reinterpret_cast<unsigned long long*>(clocks), sink, (int)iters, 1e-3f);
+  return tb::launch_status("tb_probe_clock");
 }
 
 tb_status tb_probe_read(const void* src, int64_t bytes, uint32_t key, uint32_t* sink, hipStream_t stream) {

@@ -14,6 +14,13 @@ of a dispatch is summed over the GPU, as rocprofv3 reports it).
         copy probe (tb::copy_kernel, 16 bytes per thread each way) in the same pass; merged
         into an existing traffic.json (kernels not in these passes are kept)
 
+    python -m tilebench_amd.profiling.counters table FETCH_DIR WRITE_DIR BENCH_JSON
+        the same scaled bytes per workload of a bench.py run (BENCH_JSON: the
+        JSON line that pass printed), beside the workload's algorithmic reads
+        and writes: each workload's roofline kernel, averaged over its own
+        dispatches (the run splits into workloads at the fill launches that
+        graph capture leaves before each workload's replays)
+
 Derived ratios: MFMA utilisation = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8
 XCDs x 1024 SIMDs); SQ cycle counters are in units of four cycles per wave.
 """
@@ -80,8 +87,6 @@ def derived(c: dict) -> dict:
             d["mfma_busy_cycles_per_instruction"] = c["SQ_VALU_MFMA_BUSY_CYCLES"] / c["SQ_INSTS_MFMA"]
     if c.get("SQ_WAVES") and "SQ_INSTS_VALU" in c:
         d["valu_per_wave"] = c["SQ_INSTS_VALU"] / c["SQ_WAVES"]
-    if g and "SQ_BUSY_CYCLES" in c:
-        d["sq_busy_fraction"] = c["SQ_BUSY_CYCLES"] / g
     return d
 
 
@@ -115,19 +120,76 @@ def copy_factor(path: str, counter: str) -> float:
 
 
 def traffic(fetch_dir: str, write_dir: str) -> dict:
-    """{kernel: {"fetch_bytes", "write_bytes", "fetch_factor", "write_factor"}}: KiB per
-    dispatch x 1024, scaled so that the copy probe reads its known bytes."""
+    """{kernel: {"fetch_bytes", "write_bytes", "fetch_factor", "write_factor"}} of the
+    backend's kernels (tb::): KiB per dispatch x 1024, scaled so that the copy probe
+    reads its known bytes.  The probe itself is left out (its dispatches move 512 MiB
+    or 1 GiB, so a mean over them describes neither)."""
     fetch = per_dispatch([fetch_dir])
     write = per_dispatch([write_dir])
     ff, wf = copy_factor(fetch_dir, "FETCH_SIZE"), copy_factor(write_dir, "WRITE_SIZE")
     out = {}
     for name in sorted(set(fetch) & set(write)):
-        if name == COPY_KERNEL:
+        if name == COPY_KERNEL or not name.startswith("tb::"):
             continue
         out[name] = {"fetch_bytes": int(round(fetch[name]["counters"]["FETCH_SIZE"] * 1024 * ff)),
                      "write_bytes": int(round(write[name]["counters"]["WRITE_SIZE"] * 1024 * wf)),
                      "fetch_factor": round(ff, 4), "write_factor": round(wf, 4)}
     return out
+
+
+def _dispatches(path: str, counter: str) -> list[tuple[str, float]]:
+    """[(kernel stem, counter value)] of one pass in dispatch order."""
+    rows = []
+    for f in counter_files(path):
+        with open(f, newline="") as fh:
+            rows += [(int(r["Dispatch_Id"]), kernel_stem(r["Kernel_Name"]), float(r["Counter_Value"]))
+                     for r in csv.DictReader(fh) if r["Counter_Name"] == counter]
+    rows.sort()
+    return [(k, v) for _, k, v in rows]
+
+
+def workload_table(fetch_dir: str, write_dir: str, bench_json: str) -> list[dict]:
+    """Per workload of the bench run: its roofline kernel's scaled FETCH/WRITE bytes per
+    launch (mean over the workload's own dispatches of it) and its algorithmic bytes."""
+    from tilebench_amd.profiling.suite_trace import bench_line, segments, workloads
+
+    line = bench_line(bench_json)
+    wl = workloads(line)
+    alg = {wl[0][0]: line["roofline"]}
+    alg.update(line.get("suite") or {})
+    out = []
+    per_pass = {}
+    for d, counter in ((fetch_dir, "FETCH_SIZE"), (write_dir, "WRITE_SIZE")):
+        recs = _dispatches(d, counter)
+        per_pass[counter] = (recs, segments(recs, len(wl)), copy_factor(d, counter))
+    for j, (name, kernel, _) in enumerate(wl):
+        row = {"workload": name, "kernel": kernel,
+               "alg_read_bytes": alg[name].get("alg_read_bytes"), "alg_write_bytes": alg[name].get("alg_write_bytes")}
+        for counter, key in (("FETCH_SIZE", "fetch_bytes"), ("WRITE_SIZE", "write_bytes")):
+            recs, segs, factor = per_pass[counter]
+            lo, hi = segs[j]
+            vals = [v for k, v in recs[lo:hi] if k == kernel]
+            row[key] = sum(vals) / len(vals) * 1024 * factor if vals else None
+            row["dispatches"] = len(vals)
+        out.append(row)
+    return out
+
+
+def format_table(rows: list[dict]) -> str:
+    def kib(v):
+        return "-" if v is None else f"{v / 1024:.0f}"
+
+    def ratio(a, b):
+        return "-" if a is None or not b else f"{a / b:.2f}"
+
+    lines = [f"{'workload':28s} {'kernel':42s} {'fetch_KiB':>10s} {'alg_rd_KiB':>10s} {'x':>6s} "
+             f"{'write_KiB':>10s} {'alg_wr_KiB':>10s} {'x':>6s}"]
+    for r in rows:
+        lines.append(f"{r['workload'][:28]:28s} {r['kernel'][:42]:42s} {kib(r['fetch_bytes']):>10s} "
+                     f"{kib(r['alg_read_bytes']):>10s} {ratio(r['fetch_bytes'], r['alg_read_bytes']):>6s} "
+                     f"{kib(r['write_bytes']):>10s} {kib(r['alg_write_bytes']):>10s} "
+                     f"{ratio(r['write_bytes'], r['alg_write_bytes']):>6s}")
+    return "\n".join(lines)
 
 
 def main(argv=None) -> int:
@@ -141,9 +203,16 @@ def main(argv=None) -> int:
     t.add_argument("write_dir")
     t.add_argument("--out", default=None, help="traffic.json to update (printed when omitted)")
     t.add_argument("--workload", default="", help="text stored with each updated kernel")
+    b = sub.add_parser("table")
+    b.add_argument("fetch_dir")
+    b.add_argument("write_dir")
+    b.add_argument("bench_json", help="bench.py's JSON line from one of the two passes")
     args = ap.parse_args(argv)
     if args.cmd == "summary":
         print(format_summary(per_dispatch(args.dirs, args.kernel)))
+        return 0
+    if args.cmd == "table":
+        print(format_table(workload_table(args.fetch_dir, args.write_dir, args.bench_json)))
         return 0
     new = traffic(args.fetch_dir, args.write_dir)
     if args.out is None:

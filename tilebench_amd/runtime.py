@@ -61,6 +61,7 @@ SIGNATURES: dict[str, list] = {
     "tb_probe_copy": [_c_p, _c_p, _c_i64, _c_p],
     "tb_probe_read": [_c_p, _c_i64, _c_u32, _c_p, _c_p],
     "tb_probe_mfma": [_c_int, _c_i64, _c_i64, _c_p, _c_p],
+    "tb_probe_clock": [_c_i64, _c_i64, _c_p, _c_p, _c_p],
 }
 
 #: symbols returning a C string
