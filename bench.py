@@ -212,7 +212,7 @@ def _w_fp8_quant_blocks():
                 metric="fp8 per-token 128-channel quant HBM throughput", unit="GB/s", dtype="fp16->e4m3",
                 bound="hbm", bytes=nbytes, flops=None, out_bytes=M * K + 4 * M * (K // 128),
                 inputs=lambda: T.generate_fp8_act_quant_blocks_inputs(M, K, seed=2, device="cuda"),
-                step=lambda x: impl_hip.run(*x), kernel="tb::fp8blk::fp8_quant_blocks", cpu=cpu)
+                step=lambda x: impl_hip.run(*x), kernel="tb::fp8blk::fp8_quant_blocks<2>", cpu=cpu)
 
 
 def _w_fp8_gemm():
@@ -634,7 +634,9 @@ def roofline(w, ms: float) -> dict:
     cp = calibrated_peak(w["bound"], w.get("peak_key"))
     out = {"bound": w["bound"], "achieved": round(achieved, 2), "peak": peak, "unit": unit,
            "frac": round(achieved / peak, 4), "traffic": measured_traffic(w["kernel"]),
-           "kernel": w["kernel"], "measured_peak": mp,
+           "kernel": w["kernel"], "alg_read_bytes": w["bytes"] - w.get("out_bytes", 0),
+           "alg_write_bytes": w.get("out_bytes", 0),
+           "measured_peak": mp,
            "frac_of_measured": None if mp is None else round(achieved / mp, 4),
            "calibrated_peak": cp, "frac_of_calibrated": None if cp is None else round(achieved / cp, 4)}
     if "mfma_flops" in w:

@@ -348,34 +348,53 @@ __global__ void __launch_bounds__(WAVES * 64, 1)
 // ------------------------------------------------------------------ activation quantiser
 
 // One 16-lane group per 128-element block of a row (a lane holds 8 halfs),
-// four blocks per wavefront, 16 per 256-thread block; the blocks of a row are
-// consecutive, so a wavefront reads 1 KiB of one row (or of two rows at a
-// row boundary) per load.
+// IT blocks per group: item i of workgroup b covers blocks 16 (IT b + i) ..
+// + 15, so each item's 16 groups read 4 KiB of consecutive blocks (the blocks
+// of a row are consecutive), and all IT loads of a lane are issued before the
+// first reduction.
+// Maximum over the 16 lanes of a DPP row (a lane group): rotations by 8, 4, 2
+// and 1 within the row, VALU only.
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false));  // row_ror:8
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xF, 0xF, false));  // row_ror:4
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x122, 0xF, 0xF, false));  // row_ror:2
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x121, 0xF, 0xF, false));  // row_ror:1
+  return v;
+}
+
+// The block count M * K / 128 is below 2^23 (A < 2 GiB), so block ids and
+// their row / block split fit 32-bit arithmetic.
+template <int IT>
 __global__ void __launch_bounds__(256) fp8_quant_blocks(const u32x4* __restrict__ A, u32x2* __restrict__ Aq,
-                                                        float* __restrict__ sa_out, int64_t M, int64_t nkb) {
-  const int64_t blk = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);  // global block id = m * nkb + kb
-  const int sub = threadIdx.x & 15;
-  const int64_t total = M * nkb;
-  const bool live = blk < total;
-  const buf_rsrc_t rs = buf_rsrc(A, (uint32_t)min<int64_t>(total * 256, 0x7FFFFFFFll));
-  const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs, live ? (uint32_t)((blk * 16 + sub) * 16) : BUF_OOB, 0,
-                                                        2 /* nt */);
-  uint32_t m = 0;
+                                                        float* __restrict__ sa_out, uint32_t M, uint32_t nkb) {
+  const uint32_t sub = threadIdx.x & 15, grp = threadIdx.x >> 4;
+  const uint32_t total = M * nkb;
+  const buf_rsrc_t rs = buf_rsrc(A, total * 256u);
+  u32x4 x[IT];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t a = x[j] & 0x7FFF7FFFu;
-    m = max(m, max(a & 0xFFFFu, a >> 16));
+  for (int i = 0; i < IT; ++i) {
+    const uint32_t blk = (blockIdx.x * IT + i) * 16u + grp;  // global block id = m * nkb + kb
+    x[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, blk < total ? (blk * 16u + sub) * 16u : BUF_OOB, 0, 2 /* nt */);
   }
-  // maximum over the 16 lanes of the group (xor partners stay inside it)
 #pragma unroll
-  for (int off = 8; off >= 1; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off, 64));
-  const float amax = (float)__builtin_bit_cast(_Float16, (uint16_t)m);
-  const float s = amax / 448.0f;
-  const float y = 1.0f / s;
-  if (!live) return;
-  const int64_t row = blk / nkb, kb = blk - row * nkb;
-  if (sub == 0) sa_out[kb * M + row] = s;
-  Aq[blk * 16 + sub] = quantize_chunk(x, s, y, m);
+  for (int i = 0; i < IT; ++i) {
+    const uint32_t blk = (blockIdx.x * IT + i) * 16u + grp;
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t a = x[i][j] & 0x7FFF7FFFu;
+      m = max(m, max(a & 0xFFFFu, a >> 16));
+    }
+    m = row16_max_u32(m);
+    const float amax = (float)__builtin_bit_cast(_Float16, (uint16_t)m);
+    const float s = amax / 448.0f;
+    const float y = 1.0f / s;
+    if (blk < total) {
+      const uint32_t row = blk / nkb, kb = blk - row * nkb;
+      if (sub == 0) sa_out[kb * M + row] = s;
+      Aq[blk * 16u + sub] = quantize_chunk(x[i], s, y, m);
+    }
+  }
 }
 
 template <int BN, int WAVES, int NSTAGE>
@@ -413,8 +432,13 @@ extern "C" tb_status tb_fp8_act_quant_blocks(const uint16_t* A, uint8_t* Aq, flo
   TB_CHECK_ALIGN(A, 16, "A");
   TB_CHECK_ALIGN(Aq, 8, "Aq");
   const int64_t blocks = M * (K / 128);
-  hipLaunchKernelGGL(tb::fp8blk::fp8_quant_blocks, dim3((unsigned)((blocks + 15) / 16)), dim3(256), 0, stream,
-                     reinterpret_cast<const tb::u32x4*>(A), reinterpret_cast<tb::u32x2*>(Aq), sa, M, K / 128);
+#ifndef FP8QB_IT
+#define FP8QB_IT 2
+#endif
+  constexpr int IT = FP8QB_IT;
+  hipLaunchKernelGGL(tb::fp8blk::fp8_quant_blocks<IT>, dim3((unsigned)((blocks + 16 * IT - 1) / (16 * IT))), dim3(256),
+                     0, stream, reinterpret_cast<const tb::u32x4*>(A), reinterpret_cast<tb::u32x2*>(Aq), sa,
+                     (uint32_t)M, (uint32_t)(K / 128));
   return tb::launch_status("tb_fp8_act_quant_blocks");
 }
 
