@@ -18,7 +18,9 @@ sequence of each.  One row per pair, with the reference's keys:
 With ``--all-cases`` every case of the grid is probed, and each row also lists
 the distinct launch sequences with the cases that produce them (the hip
 backend picks its kernels by shape: decode or prefill, tile size, a transpose
-fallback for odd widths).  A failed probe records count=None and the error.
+fallback for odd widths); the operator's named grids (config.yaml "grids:", as
+``run_bench --grid`` runs them) get one row each, {"op", "grid", "backend",
+"cases", "sequences"}.  A failed probe records count=None and the error.
 
 Usage:  python -m tilebench_amd.profiling.probe --out profiles/kernel_counts_hip_MI355X.json
         python -m tilebench_amd.profiling.probe --ops w4a16_gemm,matmul_int8 --all-cases
@@ -81,7 +83,8 @@ def probe_case(impl, op: str, case: dict) -> dict:
 def probe_operator(op: str, all_cases: bool = False) -> list[dict]:
     impl = importlib.import_module(f"tilebench_amd.benchmarks.operators.{op}.impl_hip")
     with open(operator_config(op)) as fh:
-        cases = expand_cases(op, yaml.safe_load(fh))
+        cfg = yaml.safe_load(fh)
+    cases = expand_cases(op, cfg)
     rows = []
     for dt in sorted({str(c.get("dtype", "fp32")) for c in cases}):
         mine = [c for c in cases if str(c.get("dtype", "fp32")) == dt]
@@ -93,18 +96,32 @@ def probe_operator(op: str, all_cases: bool = False) -> list[dict]:
         except Exception as e:  # a failing pair is recorded, the others still run
             row.update({"count": None, "error": f"{type(e).__name__}: {e}"[:200]})
         if all_cases:
-            seqs: dict[tuple, list] = {}
-            for c in mine:
-                p = {k: v for k, v in c.items() if k != "dtype"}
-                try:
-                    key = tuple(probe_case(impl, op, c)["names"])
-                except Exception as e:
-                    key = ("error: " + f"{type(e).__name__}: {e}"[:160],)
-                seqs.setdefault(key, []).append(p)
-            row["sequences"] = [{"names": list(k), "cases": v} for k, v in seqs.items()]
+            row["sequences"] = _sequences(impl, op, mine)
         rows.append(row)
         torch.cuda.empty_cache()
+    if all_cases:
+        # the operator's named grids (config "grids:"), as the engine's --grid runs them
+        for name, alt in sorted((cfg.get("grids") or {}).items()):
+            gcfg = {k: v for k, v in cfg.items() if k not in ("case_grid", "case_defaults", "test_cases")}
+            gcfg.update(alt)
+            gcases = expand_cases(op, gcfg)
+            rows.append({"op": op, "grid": name, "backend": "hip", "cases": len(gcases),
+                         "sequences": _sequences(impl, op, gcases)})
+            torch.cuda.empty_cache()
     return rows
+
+
+def _sequences(impl, op: str, cases: list[dict]) -> list[dict]:
+    """Cases grouped by the kernel sequence one call launches."""
+    seqs: dict[tuple, list] = {}
+    for c in cases:
+        p = {k: v for k, v in c.items() if k != "dtype"}
+        try:
+            key = tuple(probe_case(impl, op, c)["names"])
+        except Exception as e:
+            key = ("error: " + f"{type(e).__name__}: {e}"[:160],)
+        seqs.setdefault(key, []).append(p)
+    return [{"names": list(k), "cases": v} for k, v in seqs.items()]
 
 
 def main(argv=None) -> int:
@@ -121,19 +138,29 @@ def main(argv=None) -> int:
     for op in ops:
         print(f"probe {op}", flush=True)
         rows += probe_operator(op, args.all_cases)
+    def key(r):  # a dtype row of the default grid, or a named grid's row
+        return (r["op"], r.get("dtype") or "grid:" + r["grid"])
+
     if args.out:
         out = Path(args.out)
         if out.exists():
-            probed = {(r["op"], r["dtype"]) for r in rows}
-            rows += [r for r in json.loads(out.read_text()) if (r["op"], r["dtype"]) not in probed]
-        rows.sort(key=lambda r: (r["op"], r["dtype"]))
+            probed = {key(r) for r in rows}
+            rows += [r for r in json.loads(out.read_text()) if key(r) not in probed]
+        rows.sort(key=key)
         out.parent.mkdir(parents=True, exist_ok=True)
         out.write_text(json.dumps(rows, indent=1) + "\n")
     print(f"{'op':26s} {'dtype':11s} {'count':>5s}  first  names")
     for r in rows:
+        if "grid" in r:
+            for sq in r["sequences"]:
+                print(f"{r['op']:26s} {'grid ' + r['grid']:11s} {len(sq['cases']):>5d}  cases  "
+                      f"{', '.join(sq['names'])[:100]}")
+            continue
         print(f"{r['op']:26s} {r['dtype']:11s} {str(r['count']):>5s}  {str(r.get('first_call_identical')):5s}  "
               f"{', '.join(r.get('names') or [r.get('error', '')])[:100]}")
-    return 0 if all(r["count"] is not None for r in rows) else 1
+    failed = [r for r in rows if ("grid" not in r and r["count"] is None) or
+              any(sq["names"][0].startswith("error:") for sq in r.get("sequences") or [])]
+    return 0 if not failed else 1
 
 
 if __name__ == "__main__":
