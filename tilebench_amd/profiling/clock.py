@@ -31,7 +31,7 @@ import time
 MIB = 1024 * 1024
 
 
-def _probe_clock(rt, torch, blocks: int, iters: int, clocks, sink) -> None:
+def _probe_clock(rt, blocks: int, iters: int, clocks, sink) -> None:
     rt.call("tb_probe_clock", blocks, iters, clocks.data_ptr(), sink.data_ptr(), rt.stream_handle())
 
 
@@ -47,16 +47,16 @@ def clock_part(rt, torch, blocks: int = 1024, target_ms: float = 1.5) -> list[st
     iters = 200
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for _ in range(3):
-        _probe_clock(rt, torch, blocks, iters, bufs[0], sink)
+        _probe_clock(rt, blocks, iters, bufs[0], sink)
     e0.record()
-    _probe_clock(rt, torch, blocks, iters, bufs[0], sink)
+    _probe_clock(rt, blocks, iters, bufs[0], sink)
     e1.record()
     torch.cuda.synchronize()
     iters = max(1, int(iters * target_ms / e0.elapsed_time(e1)))
     out = [f"part 1: tb_probe_clock, {blocks} blocks x 256 threads, {iters} iterations of 8 fp16 MFMAs "
            f"(about {target_ms} ms per launch)"]
     for i in range(20):
-        _probe_clock(rt, torch, blocks, iters, bufs[i], sink)
+        _probe_clock(rt, blocks, iters, bufs[i], sink)
     torch.cuda.synchronize()
     out.append("  20 launches back to back, MHz: " + " ".join(f"{_mhz(b):.0f}" for b in bufs))
     for idle in (0.0, 0.0005, 0.002, 0.02):
@@ -67,7 +67,7 @@ def clock_part(rt, torch, blocks: int = 1024, target_ms: float = 1.5) -> list[st
                 time.sleep(idle)
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
-            _probe_clock(rt, torch, blocks, iters, bufs[i], sink)
+            _probe_clock(rt, blocks, iters, bufs[i], sink)
             b.record()
             torch.cuda.synchronize()
             mhz.append(_mhz(bufs[i]))
