@@ -369,12 +369,19 @@ __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64, 1)
 
 // B [K, N] (E = 1 or 2 bytes per element) -> B^T [N, K].  Needs N % 8 == 0 and
 // K a multiple of 16 / E; partial source chunks at the N edge fall back to
-// element loads.
+// element loads.  A tile is TILE_B / E elements square: 128 bytes of each
+// source row and of each destination row, whole 128-byte lines both ways (with
+// 64 x 64 one-byte tiles every line was read by two blocks: twice the bytes).
+constexpr int TILE_B = 128;
+// With 16-byte-aligned LDS rows, rows 16 apart share their banks; the store
+// phases read one byte from each of 8 rows 16 apart, so the 16-byte chunks of
+// a one-byte tile's row k sit at slot chunk ^ ((k >> 4) & 7) (8 different banks).
+__device__ __forceinline__ int tslot(int k, int chunk) { return chunk ^ ((k >> 4) & 7); }
 template <int E>
 __global__ void __launch_bounds__(256) transpose_tile(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
                                                       int K, int N) {
-  constexpr int T = 64, V = 16 / E;  // elements per 16-byte chunk
-  constexpr int ROW = T * E + 16;    // padded LDS row (bytes), 16-byte aligned
+  constexpr int T = TILE_B / E, V = 16 / E;  // elements per tile side, per 16-byte chunk
+  constexpr int ROW = T * E + 16;            // padded LDS row (bytes), 16-byte aligned
   __shared__ __attribute__((aligned(16))) uint8_t tile[T * ROW];
   const int k0 = blockIdx.y * T, n0 = blockIdx.x * T;
   const int t = threadIdx.x;
@@ -392,7 +399,7 @@ __global__ void __launch_bounds__(256) transpose_tile(const uint8_t* __restrict_
         v = __builtin_bit_cast(u32x4, b);
       }
     }
-    *reinterpret_cast<u32x4*>(tile + r * ROW + c * 16) = v;
+    *reinterpret_cast<u32x4*>(tile + r * ROW + (E == 1 ? tslot(r, c) : c) * 16) = v;
   }
   __syncthreads();
   for (int idx = t; idx < T * (T / V); idx += 256) {
@@ -403,7 +410,10 @@ __global__ void __launch_bounds__(256) transpose_tile(const uint8_t* __restrict_
 #pragma unroll
     for (int q = 0; q < V; ++q)
 #pragma unroll
-      for (int e = 0; e < E; ++e) b[q * E + e] = tile[(c * V + q) * ROW + r * E + e];
+      for (int e = 0; e < E; ++e) {
+        const int kr = c * V + q;
+        b[q * E + e] = E == 1 ? tile[kr * ROW + tslot(kr, r >> 4) * 16 + (r & 15)] : tile[kr * ROW + r * E + e];
+      }
     *reinterpret_cast<u32x4*>(dst + ((int64_t)n * K + k) * E) = __builtin_bit_cast(u32x4, b);
   }
 }
@@ -412,7 +422,7 @@ __global__ void __launch_bounds__(256) transpose_tile(const uint8_t* __restrict_
 // B^T[n, i*K/4 + kb] = ((packed[kb, n] >> 2i) & 3) - 1.  Needs K/4 % 16 == 0.
 __global__ void __launch_bounds__(256) unpack_i2_tile(const uint8_t* __restrict__ packed, int8_t* __restrict__ dst,
                                                       int K, int N) {
-  constexpr int T = 64, ROW = T + 16;
+  constexpr int T = TILE_B, ROW = T + 16;  // 128 packed bytes of a row in, 128 bytes of a quarter row out
   __shared__ __attribute__((aligned(16))) uint8_t tile[T * ROW];
   const int Kb = K / 4;
   const int kb0 = blockIdx.y * T, n0 = blockIdx.x * T;
@@ -431,7 +441,7 @@ __global__ void __launch_bounds__(256) unpack_i2_tile(const uint8_t* __restrict_
         v = __builtin_bit_cast(u32x4, b);
       }
     }
-    *reinterpret_cast<u32x4*>(tile + r * ROW + c * 16) = v;
+    *reinterpret_cast<u32x4*>(tile + r * ROW + tslot(r, c) * 16) = v;
   }
   __syncthreads();
   // output chunk: row n, quarter i, 16 consecutive kb
@@ -444,7 +454,10 @@ __global__ void __launch_bounds__(256) unpack_i2_tile(const uint8_t* __restrict_
     for (int q4 = 0; q4 < 4; ++q4) {
       uint32_t x = 0;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) x |= (uint32_t)tile[(c * 16 + q4 * 4 + q) * ROW + r] << (8 * q);
+      for (int q = 0; q < 4; ++q) {
+        const int kr = c * 16 + q4 * 4 + q;
+        x |= (uint32_t)tile[kr * ROW + tslot(kr, r >> 4) * 16 + (r & 15)] << (8 * q);
+      }
       // field i of four bytes at once, minus one per byte without carries: (f + 0x7F) ^ 0x80 = f - 1
       w[q4] = (((x >> (2 * i)) & 0x03030303u) + 0x7F7F7F7Fu) ^ 0x80808080u;
     }
@@ -633,7 +646,8 @@ extern "C" tb_status tb_matmul(int dtype, const void* a, const void* b, void* ou
     return launch_nt<KIND_F16, OUT_F16, 128, 128, 64, 64>(reinterpret_cast<const uint8_t*>(a), ws, out, nullptr,
                                                           nullptr, M, N, kb, stream, "tb_matmul(fp16)");
   }
-  hipLaunchKernelGGL(transpose_tile<1>, tgrid, dim3(256), 0, stream, reinterpret_cast<const uint8_t*>(b), ws, (int)K,
+  const dim3 tgrid1((unsigned)((N + TILE_B - 1) / TILE_B), (unsigned)((K + TILE_B - 1) / TILE_B));
+  hipLaunchKernelGGL(transpose_tile<1>, tgrid1, dim3(256), 0, stream, reinterpret_cast<const uint8_t*>(b), ws, (int)K,
                      (int)N);
   return tb_matmul_fp8_bt(reinterpret_cast<const uint8_t*>(a), ws, reinterpret_cast<uint8_t*>(out), M, N, K, stream);
 }
@@ -655,7 +669,7 @@ extern "C" tb_status tb_matmul_int8(const int8_t* a, const uint8_t* b, int32_t* 
   TB_CHECK_ALIGN(workspace, 256, "workspace");
   TB_CHECK_ALIGN(out, 16, "out");
   int8_t* bt = reinterpret_cast<int8_t*>(workspace);
-  hipLaunchKernelGGL(unpack_i2_tile, dim3((unsigned)((N + 63) / 64), (unsigned)((K / 4 + 63) / 64)), dim3(256), 0,
+  hipLaunchKernelGGL(unpack_i2_tile, dim3((unsigned)((N + TILE_B - 1) / TILE_B), (unsigned)((K / 4 + TILE_B - 1) / TILE_B)), dim3(256), 0,
                      stream, b, bt, (int)K, (int)N);
   const int splits = int8_splits(M, N, K);
   if (splits > 1) {
