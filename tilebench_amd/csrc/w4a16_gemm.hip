@@ -1075,7 +1075,17 @@ __device__ __forceinline__ void tile4(uint8_t* __restrict__ lds, const _Float16*
     o[q] = as_u32((as_h2(and_or(d, 0x00F000F0u, c54)) - as_h2(zO)) * as_h2(sO));
   };
 
-  constexpr int VM1 = DMA_PER_STEP, VM2 = 2 * DMA_PER_STEP;
+  // A step's DMAs go out in four parts, one per slice, so that the four
+  // wavefronts of a CU never queue a whole step's loads at the texture unit at
+  // once: part 0 (PA instructions) of step kt + 3 in the slice after step kt's
+  // barrier (stage kt % 3 is free from that barrier on), parts 1..3 (PB each)
+  // in slices 1..3 of step kt + 1, before its barrier.  At a barrier the
+  // outstanding loads are then the next step's whole stage, DMA_PER_STEP of
+  // them, as before.
+  constexpr int PB = DMA_PER_STEP / 4, PA = DMA_PER_STEP - 3 * PB;
+  constexpr int DMA_GAP = NQ / (PA > PB ? PA : PB);  // MFMAs between two DMAs of a part
+  static_assert(DMA_GAP >= 1 && (PA - 1) * DMA_GAP < NQ && (PB - 1) * DMA_GAP < NQ, "DMA slots");
+  constexpr int VM1 = DMA_PER_STEP, VM2 = DMA_PER_STEP + PA;
   constexpr int WAIT_BAR = (VM1 & 15) | ((VM1 >> 4) << 14) | (7 << 4) | (0 << 8);
   constexpr int WAIT_PRO = (VM2 & 15) | ((VM2 >> 4) << 14) | (7 << 4) | (0 << 8);
   auto barrier = [&]() __attribute__((always_inline)) {
@@ -1084,10 +1094,11 @@ __device__ __forceinline__ void tile4(uint8_t* __restrict__ lds, const _Float16*
     asm volatile("" ::: "memory");
   };
 
+  // stages 0 and 1 whole, part 0 of stage 2 (its other parts go out in step 0)
 #pragma unroll
   for (int st = 0; st < 3; ++st)
 #pragma unroll
-    for (int d = 0; d < DMA_PER_STEP; ++d) issue_one(st, st, d);
+    for (int d = 0; d < (st < 2 ? DMA_PER_STEP : PA); ++d) issue_one(st, st, d);
   __builtin_amdgcn_s_waitcnt(WAIT_PRO);
   barrier();
   load_scales(0);
@@ -1152,23 +1163,25 @@ __device__ __forceinline__ void tile4(uint8_t* __restrict__ lds, const _Float16*
     wf[cur ^ 1][0] = __builtin_bit_cast(h8, e);
     wf[cur ^ 1][1] = __builtin_bit_cast(h8, o);
   };
-  auto none = [](int) {};
 
   auto step = [&](int kt, auto stc) __attribute__((always_inline)) {
     constexpr int ST = decltype(stc)::value;
-    constexpr int NST = (ST + 1) % 3;
-    slice(0, ST, 1, none);
-    slice(1, ST, 2, none);
-    slice(0, ST, 3, none);
+    constexpr int NST = (ST + 1) % 3, PST = (ST + 2) % 3;
+    // parts 1..3 of step kt + 2 into stage PST (free since step kt - 1's barrier)
+    auto part = [&](int j) __attribute__((always_inline)) {
+      return [&, j](int q) __attribute__((always_inline)) {
+        if (q % DMA_GAP == 0 && q / DMA_GAP < PB) issue_one(kt + 2, PST, PA + (j - 1) * PB + q / DMA_GAP);
+      };
+    };
+    slice(0, ST, 1, part(1));
+    slice(1, ST, 2, part(2));
+    slice(0, ST, 3, part(3));
     __builtin_amdgcn_s_waitcnt(WAIT_BAR);
     barrier();
     load_scales(NST);
+    // part 0 of step kt + 3 into stage ST (free from this barrier on)
     slice(1, NST, 0, [&](int q) {
-      issue_one(kt + 3, ST, q);
-      if (q == NQ - 1) {
-#pragma unroll
-        for (int d = NQ; d < DMA_PER_STEP; ++d) issue_one(kt + 3, ST, d);
-      }
+      if (q % DMA_GAP == 0 && q / DMA_GAP < PA) issue_one(kt + 3, ST, q / DMA_GAP);
     });
   };
   int kt = 0;
