@@ -303,6 +303,16 @@ def test_w4a16_gemm_matches_oracle(gpu, M, K, N, G):
     _w4a16_check(gpu, M, K, N, G, seed=M + N)
 
 
+@pytest.mark.parametrize("M,K,N,G", [(257, 64, 520, 64), (257, 128, 520, 64), (257, 192, 520, 64),
+                                     (257, 320, 520, 64), (3000, 192, 11008, 64)])
+def test_w4a16_prefill_short_k(gpu, M, K, N, G):
+    """Prefill K loops of 1, 2, 3 and 5 steps: a step's loads go out in four
+    parts spread over two steps, the prologue issues only the first part of the
+    third stage, and every load past the last step reads nothing.  M = 3000 x
+    N = 11008 also runs the 192-row tiles (its last tile columns)."""
+    _w4a16_check(gpu, M, K, N, G, seed=M + K)
+
+
 def test_w4a16_gemm_full_prefill(gpu):
     """BASELINE config 1 at M = 4096: checked against the oracle on a row sample
     (the full fp32 CPU product takes minutes) and for finiteness everywhere."""
@@ -670,7 +680,8 @@ def test_golden_fixtures_on_gpu(gpu):
 # ----------------------------------------------------------------------------- grouped MoE W4A16
 
 @pytest.mark.parametrize("tokens,topk,E,K,N,pad", [(512, 2, 8, 256, 1408, 128), (300, 4, 16, 512, 264, 16),
-                                                    (64, 1, 4, 128, 64, 64), (1000, 8, 64, 256, 512, 128)])
+                                                    (64, 1, 4, 128, 64, 64), (1000, 8, 64, 256, 512, 128),
+                                                    (400, 2, 8, 384, 1408, 128)])
 def test_grouped_gemm_matches_oracle(gpu, tokens, topk, E, K, N, pad):
     from tilebench_amd.benchmarks.operators.moe_w4a16_grouped_gemm import impl_hip
 
