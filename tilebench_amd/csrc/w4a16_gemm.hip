@@ -733,8 +733,19 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
     o[q] = as_u32((as_h2(and_or(d, 0x00F000F0u, c54)) - as_h2(zO)) * as_h2(sO));
   };
 
+  // A step's DMAs go out in four parts, one per slice, so that the eight
+  // wavefronts of a CU never queue a whole step's loads at the texture unit at
+  // once: part 0 (PA instructions) of step kt + 3 in the slice after step kt's
+  // barrier (stage kt % 3 is free from that barrier on), parts 1..3 (PB each)
+  // in slices 1..3 of step kt + 1, before its barrier.  At a barrier the
+  // outstanding loads are then the next step's whole stage, DMA_PER_STEP of
+  // them, as before.
+  constexpr int NQ = 2 * MB;
+  constexpr int PB = DMA_PER_STEP / 4, PA = DMA_PER_STEP - 3 * PB;
+  constexpr int DMA_GAP = NQ / (PA > PB ? PA : PB);  // MFMAs between two DMAs of a part
+  static_assert(DMA_GAP >= 1 && (PA - 1) * DMA_GAP < NQ && (PB - 1) * DMA_GAP < NQ, "DMA slots");
   // vmcnt(n) with lgkmcnt(0) (vmcnt is split: bits 3:0 and 15:14)
-  constexpr int VM1 = DMA_PER_STEP, VM2 = 2 * DMA_PER_STEP;
+  constexpr int VM1 = DMA_PER_STEP, VM2 = DMA_PER_STEP + PA;
   constexpr int WAIT_BAR = (VM1 & 15) | ((VM1 >> 4) << 14) | (7 << 4) | (0 << 8);
   constexpr int WAIT_PRO = (VM2 & 15) | ((VM2 >> 4) << 14) | (7 << 4) | (0 << 8);
   // The barrier: the compiler may not move LDS accesses across it (the empty
@@ -745,10 +756,12 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
     asm volatile("" ::: "memory");
   };
 
-  // prologue: steps 0, 1 and 2 in flight, step 0 landed, slice 0 read
+  // prologue: steps 0 and 1 and part 0 of step 2 in flight (its other parts go
+  // out in step 0), step 0 landed, slice 0 read
   issue(0, 0);
   issue(1, 1);
-  issue(2, 2);
+#pragma unroll
+  for (int d = 0; d < PA; ++d) issue_one(2, 2, d);
   __builtin_amdgcn_s_waitcnt(WAIT_PRO);
   barrier();
   load_scales(0);
@@ -794,16 +807,21 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
     wf[cur ^ 1][0] = __builtin_bit_cast(h8, e);
     wf[cur ^ 1][1] = __builtin_bit_cast(h8, o);
   };
-  auto none = [](int) {};
 
   // Step kt on stage ST = kt % 3 (a compile-time constant in each unrolled copy).
   auto step = [&](int kt, auto stc) __attribute__((always_inline)) {
     constexpr int ST = decltype(stc)::value;
-    constexpr int NST = (ST + 1) % 3;
-    slice(0, ST, 1, none);
-    slice(1, ST, 2, none);
+    constexpr int NST = (ST + 1) % 3, PST = (ST + 2) % 3;
+    // parts 1..3 of step kt + 2 into stage PST (free since step kt - 1's barrier)
+    auto part = [&](int jp) __attribute__((always_inline)) {
+      return [&, jp](int q) __attribute__((always_inline)) {
+        if (q % DMA_GAP == 0 && q / DMA_GAP < PB) issue_one(kt + 2, PST, PA + (jp - 1) * PB + q / DMA_GAP);
+      };
+    };
+    slice(0, ST, 1, part(1));
+    slice(1, ST, 2, part(2));
     if (w >= 4) __builtin_amdgcn_s_setprio(0);
-    slice(0, ST, 3, none);
+    slice(0, ST, 3, part(3));
     // step kt + 1 landed (each wavefront waits for its own DMA, only step
     // kt + 2's may still be in flight; the barrier publishes all of them) and
     // every wavefront has its stage-ST fragments in registers
@@ -815,12 +833,9 @@ __device__ __forceinline__ void tile8(uint8_t* __restrict__ lds, const _Float16*
     // barrier, the older one the last, so both arrive together.
     if (w >= 4) __builtin_amdgcn_s_setprio(1);
     load_scales(NST);
+    // part 0 of step kt + 3 into stage ST (free from this barrier on)
     slice(1, NST, 0, [&](int q) {
-      issue_one(kt + 3, ST, q);
-      if (q == 2 * MB - 1) {
-#pragma unroll
-        for (int d = 2 * MB; d < DMA_PER_STEP; ++d) issue_one(kt + 3, ST, d);
-      }
+      if (q % DMA_GAP == 0 && q / DMA_GAP < PA) issue_one(kt + 3, ST, q / DMA_GAP);
     });
   };
   int kt = 0;
