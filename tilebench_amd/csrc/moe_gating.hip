@@ -177,12 +177,9 @@ __device__ __forceinline__ float np_sum(const float (&e)[N], int n) {
 }
 
 constexpr int kBlock = 256;
-#ifndef TB_FILTER_BLOCK
-#define TB_FILTER_BLOCK 64
-#endif
 // Threads per filter-kernel block: one wavefront (measured 1-4 % faster than
 // blocks of 128 or 256 threads).
-constexpr int kFilterBlock = TB_FILTER_BLOCK;
+constexpr int kFilterBlock = 64;
 
 // Exchange with the partner lane of butterfly step `step` inside a group of
 // LPR lanes.  Steps 0-3 (partners within 16 lanes) are DPP moves: quad swaps
