@@ -643,6 +643,30 @@ def test_fp8_gemm_rounding_ties_and_specials(gpu):
     assert np.isnan(gotf[2]).all() and np.isnan(gotf[3, 5]) and gotf[0, 5] == np.inf and gotf[1, 5] == -np.inf
 
 
+def test_host_tensors_are_refused(gpu):
+    """A host tensor among the inputs raises ValueError before any launch (its
+    address would otherwise reach a kernel as a device address)."""
+    from tilebench_amd.benchmarks.operators.fp8_scaled_gemm import impl_hip as f8
+    from tilebench_amd.benchmarks.operators.int4_dequant import impl_hip as dq
+    from tilebench_amd.benchmarks.operators.moe_topk_gating import impl_hip as gt
+    from tilebench_amd.benchmarks.operators.w4a16_gemm import impl_hip as wg
+
+    _say("host tensors refused")
+    p, s, z, K, N, G = T.generate_int4_dequant_inputs(256, 64, 128, seed=1, device="cpu")
+    with pytest.raises(ValueError, match="is on cpu"):
+        dq.run(p.to(gpu), s, z.to(gpu), K, N, G)
+    A, wp, ws, wz, G = T.generate_w4a16_gemm_inputs(32, 256, 64, 128, seed=2, device="cpu")
+    with pytest.raises(ValueError, match="input 0 is on cpu"):
+        wg.run(A, wp.to(gpu), ws.to(gpu), wz.to(gpu), G)
+    logits, M, E, k = T.generate_moe_topk_gating_inputs(64, 64, 8, seed=3, device="cpu")
+    with pytest.raises(ValueError, match="is on cpu"):
+        gt.run(logits, M, E, k)
+    Aq, Wq, sa, sw = T.generate_fp8_scaled_gemm_inputs(256, 256, 128, seed=4, device="cpu")
+    with pytest.raises(ValueError, match="input 3 is on cpu"):
+        f8.run(Aq.to(gpu), Wq.to(gpu), sa.to(gpu), sw)
+    torch.cuda.synchronize()
+
+
 def test_golden_fixtures_on_gpu(gpu):
     """Every committed golden fixture reproduced by the GPU kernels."""
     import os

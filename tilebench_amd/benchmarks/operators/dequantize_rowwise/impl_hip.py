@@ -7,7 +7,7 @@ rt.load_library()
 
 
 def run(x: torch.Tensor, state_x: torch.Tensor, **kwargs):
-    rt.require_device()
+    rt.require_device(x, state_x)
     if x.dtype != torch.int8 or state_x.dtype != torch.float32:
         raise TypeError("dequantize_rowwise expects int8 x and fp32 state_x")
     x, state_x = x.contiguous(), state_x.contiguous()

@@ -10,7 +10,7 @@ _last_config = None
 
 def run(A: torch.Tensor, **kwargs):
     global _last_config
-    rt.require_device()
+    rt.require_device(A)
     if A.dtype != torch.float16 or A.dim() != 2:
         raise TypeError("fp8_act_quant expects a 2-D fp16 tensor")
     A = A.contiguous()

@@ -11,7 +11,7 @@ _last_config = None
 
 def run(A: torch.Tensor, **kwargs):
     global _last_config
-    rt.require_device()
+    rt.require_device(A)
     if A.dtype != torch.float16 or A.dim() != 2:
         raise TypeError("fp8_act_quant_blocks expects a 2-D fp16 tensor")
     M, K = A.shape

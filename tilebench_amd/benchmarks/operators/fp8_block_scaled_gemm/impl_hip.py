@@ -16,7 +16,7 @@ _last_config = None
 
 def run(Aq: torch.Tensor, WqT: torch.Tensor, sa: torch.Tensor, sw: torch.Tensor, **kwargs):
     global _last_config
-    rt.require_device()
+    rt.require_device(Aq, WqT, sa, sw)
     if Aq.dtype != torch.float8_e4m3fn or WqT.dtype != torch.float8_e4m3fn:
         raise TypeError("fp8_block_scaled_gemm expects float8_e4m3fn operands")
     M, K = Aq.shape

@@ -20,7 +20,7 @@ def workspace_size(tokens: int, topk: int, experts: int, H: int, I: int) -> int:
 
 def run(X, logits, W13, S13, Z13, W2, S2, Z2, topk: int, group13: int, group2: int, **kwargs):
     global _last_config
-    rt.require_device()
+    rt.require_device(X, logits, W13, S13, Z13, W2, S2, Z2)
     if X.dtype != torch.float16 or logits.dtype != torch.float32:
         raise TypeError("fused_moe_w4a16 expects fp16 X and fp32 router logits")
     if any(t.dtype != torch.uint8 for t in (W13, Z13, W2, Z2)) or S13.dtype != torch.float16 \

@@ -14,7 +14,7 @@ _last_config = None
 
 def run(packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, K: int, N: int, group: int, **kwargs):
     global _last_config
-    rt.require_device()
+    rt.require_device(packed, scales, zeros)
     if packed.dtype != torch.uint8 or zeros.dtype != torch.uint8 or scales.dtype != torch.float16:
         raise TypeError("int4_dequant expects uint8 packed/zeros and fp16 scales")
     if tuple(packed.shape) != (K, N // 2) or tuple(scales.shape) != (K // group, N) \

@@ -19,7 +19,7 @@ _DT = {torch.float32: 0, torch.float16: 1, torch.float8_e4m3fn: 2}
 
 
 def run(a: torch.Tensor, b: torch.Tensor, **kwargs):
-    rt.require_device()
+    rt.require_device(a, b)
     if a.dtype not in _DT or b.dtype != a.dtype:
         raise TypeError(f"matmul_fp32_fp16_fp8: unsupported dtypes {a.dtype} / {b.dtype}")
     a = a.contiguous()

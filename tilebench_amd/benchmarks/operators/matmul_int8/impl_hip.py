@@ -8,7 +8,7 @@ rt.load_library()
 
 
 def run(a: torch.Tensor, b: torch.Tensor, **kwargs):
-    rt.require_device()
+    rt.require_device(a, b)
     if a.dtype != torch.int8 or b.dtype != torch.uint8:
         raise TypeError("matmul_int8 expects int8 a and uint8 b")
     a, b = a.contiguous(), b.contiguous()

@@ -11,7 +11,7 @@ _last_config = None
 
 def run(logits: torch.Tensor, M: int, E: int, k: int, **kwargs):
     global _last_config
-    rt.require_device()
+    rt.require_device(logits)
     if logits.dtype not in _DTYPES:
         raise TypeError(f"moe_topk_gating: unsupported logits dtype {logits.dtype}")
     if tuple(logits.shape) != (M, E):

@@ -11,7 +11,7 @@ _last_config = None
 def run(A: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, offsets: torch.Tensor,
         group: int, **kwargs):
     global _last_config
-    rt.require_device()
+    rt.require_device(A, packed, scales, zeros, offsets)
     if A.dtype != torch.float16 or packed.dtype != torch.uint8 or zeros.dtype != torch.uint8 \
             or scales.dtype != torch.float16:
         raise TypeError("moe_w4a16_grouped_gemm expects fp16 A/scales and uint8 packed weights/zeros")

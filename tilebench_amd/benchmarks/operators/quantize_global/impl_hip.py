@@ -9,7 +9,7 @@ rt.load_library()
 
 
 def run(x: torch.Tensor, block_size: int = 1024, **kwargs):
-    rt.require_device()
+    rt.require_device(x)
     if x.dtype != torch.float32:
         raise TypeError("quantize_global expects fp32 input")
     x = x.contiguous()

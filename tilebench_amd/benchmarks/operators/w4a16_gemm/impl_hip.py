@@ -49,7 +49,7 @@ def _weight_shape(packed: torch.Tensor, K: int):
 def run(A: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, group: int, **kwargs):
     """Y = A @ dequant(packed) in fp16 (fp32 accumulation)."""
     global _last_config
-    rt.require_device()
+    rt.require_device(A, packed, scales, zeros)
     if A.dtype != torch.float16 or packed.dtype != torch.uint8 or zeros.dtype != torch.uint8 \
             or scales.dtype != torch.float16:
         raise TypeError("w4a16_gemm expects fp16 A/scales and uint8 packed weights/zeros")

@@ -9,7 +9,7 @@ _DT = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
 
 def run(X: torch.Tensor, S: torch.Tensor, M: int, N: int, TILE_SIZE: int, **kwargs):
-    rt.require_device()
+    rt.require_device(X, S)
     if X.dtype not in _DT or S.dtype != X.dtype:
         raise TypeError(f"weight_dequant: unsupported dtypes {X.dtype} / {S.dtype}")
     X, S = X.contiguous(), S.contiguous()

@@ -114,19 +114,26 @@ def check(status: int, what: str) -> None:
 _device_checked = False
 
 
-def require_device() -> None:
-    """Fail loudly unless the current device is a gfx950 GPU."""
+def require_device(*tensors) -> None:
+    """Fail loudly unless the current device is a gfx950 GPU and every given
+    tensor lives on it.  The kernels take raw addresses and launch on the
+    current device: a host tensor's pointer would reach a kernel as a device
+    address, so it is refused here with a ValueError instead."""
     global _device_checked
-    if _device_checked:
-        return
     import torch
 
-    if not torch.cuda.is_available() or not torch.version.hip:
-        raise HipBackendUnavailable("the hip backend needs a ROCm GPU (torch.cuda is unavailable)")
-    arch = (getattr(torch.cuda.get_device_properties(torch.cuda.current_device()), "gcnArchName", "") or "")
-    if not arch.startswith("gfx950"):
-        raise HipBackendUnavailable(f"libtbhip.so is built for gfx950, the device is {arch!r}")
-    _device_checked = True
+    if not _device_checked:
+        if not torch.cuda.is_available() or not torch.version.hip:
+            raise HipBackendUnavailable("the hip backend needs a ROCm GPU (torch.cuda is unavailable)")
+        arch = (getattr(torch.cuda.get_device_properties(torch.cuda.current_device()), "gcnArchName", "") or "")
+        if not arch.startswith("gfx950"):
+            raise HipBackendUnavailable(f"libtbhip.so is built for gfx950, the device is {arch!r}")
+        _device_checked = True
+    if tensors:
+        here = torch.cuda.current_device()
+        for i, t in enumerate(tensors):
+            if isinstance(t, torch.Tensor) and (t.device.type != "cuda" or t.device.index != here):
+                raise ValueError(f"hip backend: input {i} is on {t.device}, the kernels run on cuda:{here}")
 
 
 def stream_handle(device=None) -> int:
