@@ -118,27 +118,34 @@ __global__ void __launch_bounds__(256) dequant_rowwise_vec(const int8_t* __restr
 // One row per blockIdx.y, 4096 elements per block: thread t converts elements
 // t*8 .. t*8+7 and 2048 + t*8 .. +7 of the chunk, so each 8-byte load and each
 // 16-byte store instruction of a wavefront covers one contiguous span (512 B
-// read, 1 KiB written), and no thread divides to find its row.
+// read, 1 KiB written), and no thread divides to find its row.  Both loads go
+// out before any branch (a lane past the row reads the row's first bytes and
+// stores nothing), so they are in flight together.
 __global__ void __launch_bounds__(256) dequant_rowwise_rows(const int8_t* __restrict__ x, const float* __restrict__ state,
                                                             uint16_t* __restrict__ y, int64_t cols) {
   const int64_t r = blockIdx.y;
   const float s = state[r];
   const float inv127 = 1.0f / 127.0f;
+  int64_t c[2];
+  u32x2 xv[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const int64_t c = (int64_t)blockIdx.x * 4096 + h * 2048 + threadIdx.x * 8;
-    if (c >= cols) continue;  // cols % 16 == 0: a thread's 8 elements are all in or all out
-    const u32x2 xv = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(x + r * cols + c));
+    c[h] = (int64_t)blockIdx.x * 4096 + h * 2048 + threadIdx.x * 8;
+    // cols % 16 == 0: a thread's 8 elements are all in or all out
+    xv[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(x + r * cols + (c[h] < cols ? c[h] : 0)));
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
     u32x4 o;
 #pragma unroll
     for (int q = 0; q < 2; ++q)
 #pragma unroll
       for (int b = 0; b < 4; b += 2) {
-        const float a0 = (s * (float)(int8_t)((xv[q] >> (8 * b)) & 0xFFu)) * inv127;
-        const float a1 = (s * (float)(int8_t)((xv[q] >> (8 * (b + 1))) & 0xFFu)) * inv127;
+        const float a0 = (s * (float)(int8_t)((xv[h][q] >> (8 * b)) & 0xFFu)) * inv127;
+        const float a1 = (s * (float)(int8_t)((xv[h][q] >> (8 * (b + 1))) & 0xFFu)) * inv127;
         o[q * 2 + (b >> 1)] = (uint32_t)f_to_h_of_rounded(a0) | ((uint32_t)f_to_h_of_rounded(a1) << 16);
       }
-    st_nt(reinterpret_cast<u32x4*>(y + r * cols + c), o);
+    if (c[h] < cols) st_nt(reinterpret_cast<u32x4*>(y + r * cols + c[h]), o);
   }
 }
 
