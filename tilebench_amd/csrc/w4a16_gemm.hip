@@ -450,7 +450,12 @@ constexpr int Z_OFF = S_OFF + BN * 2;     // 256 B: its zero-points (128 B) + 12
 constexpr int PAD_OFF = Z_OFF + 256;      // 256 B: landing pad of the idle wavefronts' DMA
 constexpr int W_ST = PAD_OFF + 256;       // 9 KiB per W stage
 constexpr int STAGE = A_ST + W_ST;
-constexpr size_t LDS_BYTES = (size_t)STAGES * STAGE;  // 123 KiB
+// The plain tile4 epilogue stages its fp16 output tile in LDS (rows of
+// C_STRIDE halves, a 16-byte pad) over the stages, which it no longer needs.
+constexpr int C_STRIDE = BN + 8;
+constexpr size_t RING_BYTES = (size_t)STAGES * STAGE;  // 123 KiB
+constexpr size_t C_BYTES = (size_t)BM * C_STRIDE * 2;  // 132 KiB
+constexpr size_t LDS_BYTES = RING_BYTES > C_BYTES ? RING_BYTES : C_BYTES;
 static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 
 typedef int v2i __attribute__((ext_vector_type(2)));
@@ -1236,6 +1241,39 @@ __device__ __forceinline__ void tile4(uint8_t* __restrict__ lds, const _Float16*
         }
         if (m < M && acol < I) *reinterpret_cast<u32x4*>(Y + (int64_t)m * I + acol) = v;
       }
+    }
+    return;
+  }
+  if constexpr (MODE == T_PLAIN) {
+    // The tile goes through LDS so that the stores write whole rows: a
+    // wavefront's 16-byte store instruction covers 2 rows x 512 bytes instead
+    // of 32 bytes of each of 32 rows.  Every wavefront has finished reading
+    // the stages (the DMAs past the last step were waited for above).
+    constexpr int TN = 64 * WN;  // tile columns
+    __syncthreads();
+    typedef __attribute__((address_space(3))) uint8_t lds_u8;
+    lds_u8* const cbase = (lds_u8*)(__attribute__((address_space(3))) void*)lds;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int r = 32 * (MB * wm + mb) + j;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        u32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] = as_u32(f16x2{(_Float16)acc[mb][0][4 * g + e], (_Float16)acc[mb][1][4 * g + e]});
+        // columns 64 wn + 16 g + 8 h .. +7 of row r
+        *(__attribute__((address_space(3))) u32x4*)(cbase + (r * C_STRIDE + 64 * wn + 16 * g + 8 * h) * 2) = v;
+      }
+    }
+    __syncthreads();  // the LDS writes of every wavefront have landed
+    const int rows = min(TM, M - tile.m0), cols = min(TN, N - tile.n0);
+    constexpr int CPR = TN / 8;  // 16-byte chunks per row
+#pragma unroll 4
+    for (int idx = t; idx < TM * CPR; idx += 256) {
+      const int r = idx / CPR, ch = idx % CPR;
+      const u32x4 v = *(__attribute__((address_space(3))) const u32x4*)(cbase + (r * C_STRIDE + ch * 8) * 2);
+      if (r < rows && ch * 8 < cols) *reinterpret_cast<u32x4*>(Y + (int64_t)(tile.m0 + r) * N + tile.n0 + ch * 8) = v;
     }
     return;
   }
