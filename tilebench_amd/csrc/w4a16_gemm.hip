@@ -26,11 +26,15 @@
 //           half2 from the 0x64 / 0x54 magic numbers, exact zero-point
 //           subtraction, one RNE multiply by the scale);
 //   MFMA  : while the MFMAs of one slice run (16 in tile4, 8 in tile8), the
-//           wavefront reads and dequantises the next slice; the DMA of step
-//           k + 3 is issued between the MFMAs that follow the step's barrier;
+//           wavefront reads and dequantises the next slice; a step's DMAs go
+//           out in four parts between the MFMAs of four slices (the first
+//           part of step k + 3 after step k's barrier, the rest during step
+//           k + 1), so a CU never queues a whole step's loads at once;
 //   output: each lane holds 8 consecutive columns of one row per accumulator
-//           group (even and odd accumulators interleaved): 16-byte stores
-//           straight from the accumulators.
+//           group (even and odd accumulators interleaved).  The plain tile4
+//           epilogue (dense and grouped GEMMs) stages the fp16 tile in LDS and
+//           stores whole row runs; the MoE epilogues store 16 bytes straight
+//           from the accumulators.
 //   rounds: a launch of T tiles on C CUs runs ceil(T / C) rounds; when the
 //           last round would be part-empty, the host may cover the last tile
 //           columns with 192-row tiles instead, so that the work splits into
