@@ -119,6 +119,18 @@ def _filter_rows(E):
     rows.append(r)
     r = np.full(E, 3.0, np.float32)                          # every element tied
     rows.append(r)
+    # Candidates whose order keys differ only in their low five bits (the
+    # candidate sort's short keys hold their list slots there): the larger
+    # value at the higher index (short-key order wrong, the wavefront re-sorts
+    # the exact pairs), at the lower index (short-key order right), and three
+    # negative values of which the middle index is the largest.
+    up = lambda v: np.nextafter(np.float32(v), np.float32(np.inf))
+    r = rng.standard_normal(E).astype(np.float32); r[3] = 4.0; r[E - 5] = up(4.0)
+    rows.append(r)
+    r = rng.standard_normal(E).astype(np.float32); r[E - 5] = 4.0; r[3] = up(4.0)
+    rows.append(r)
+    r = base(); r[[1, 22, 43]] = -0.5; r[22] = up(-0.5)
+    rows.append(r)
     return np.stack(rows)
 
 
@@ -136,7 +148,7 @@ def test_gating_filter_paths(gpu, E, k):
     rng = np.random.default_rng(100 * E + k)
     x = rng.standard_normal((1001, E)).astype(np.float32)
     special = _filter_rows(E)
-    x[17:17 + len(special)] = special            # in the wavefronts of rows 16..19, 20..23, 24..27
+    x[17:17 + len(special)] = special            # in the wavefronts of rows 16..19 to 28..31
     x[600:600 + len(special)] = special[::-1]
     w, i = impl_hip.run(torch.from_numpy(x).to(gpu), x.shape[0], E, k)
     torch.cuda.synchronize()

@@ -529,6 +529,26 @@ __device__ __forceinline__ void sort16_desc_g(int32_t (&v)[G], int p) {
   TB_STAGE((cxf4_i32(x, p)))
   TB_STAGE((cxf_i32<0x4E, 2>(x, p)))
   TB_STAGE((cxf_i32<0xB1, 1>(x, p)))
+}
+
+// The 8th largest of the 16 values of a row, in every lane of the row, for G
+// rows per lane group.  The first six stages of sort16_desc sort each 8-lane
+// half descending (a, b); the larger of lane i and its mirror 15 - i,
+// max(a[i], b[7 - i]), leaves the row's eight largest values in each half (the
+// bitonic merge's first step), and their minimum is reduced over the half:
+// 22 VALU operations per row against 31 for the full sort and a broadcast.
+template <int G>
+__device__ __forceinline__ void eighth_of16_g(int32_t (&v)[G], int p) {
+  TB_STAGE((cxf_i32<0xB1, 1>(x, p)))
+  TB_STAGE((cxf_i32<0x1B, 2>(x, p)))
+  TB_STAGE((cxf_i32<0xB1, 1>(x, p)))
+  TB_STAGE((cxf_i32<0x141, 4>(x, p)))
+  TB_STAGE((cxf_i32<0x4E, 2>(x, p)))
+  TB_STAGE((cxf_i32<0xB1, 1>(x, p)))
+  TB_STAGE((max(x, dpp_i32<0x140>(x))))  // row_mirror: lane 15 - i
+  TB_STAGE((min(x, dpp_i32<0xB1>(x))))   // lane i ^ 1
+  TB_STAGE((min(x, dpp_i32<0x4E>(x))))   // lane i ^ 2
+  TB_STAGE((min(x, dpp_i32<0x141>(x))))  // row_half_mirror: the other quad of the half
 #undef TB_STAGE
 }
 
@@ -638,11 +658,17 @@ __global__ void __launch_bounds__(kFilterBlock) filter_kernel(const void* __rest
 
   // T = the k-th largest lane maximum of the row (k <= KMAX = 8): the k lanes
   // above it hold k elements >= T, so every element the top-k can select is >= T.
-  sort16_desc_g<G>(kmax, q);
+  constexpr bool EIGHTH = KFIX && KMAX == 8;
+  if constexpr (EIGHTH)
+    eighth_of16_g<G>(kmax, q);
+  else
+    sort16_desc_g<G>(kmax, q);
   float T[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const int32_t tk = KFIX ? (int32_t)row_bcast<KMAX - 1>((uint32_t)kmax[g]) : row_lane(kmax[g], k - 1);
+    const int32_t tk = EIGHTH ? kmax[g]
+                       : KFIX ? (int32_t)row_bcast<KMAX - 1>((uint32_t)kmax[g])
+                              : row_lane(kmax[g], k - 1);
     T[g] = __builtin_bit_cast(float, (uint32_t)flip_key((uint32_t)tk));
   }
 
@@ -729,8 +755,34 @@ __global__ void __launch_bounds__(kFilterBlock) filter_kernel(const void* __rest
       big = big || (live[g] && total[g] > LPR);
     }
     if (__builtin_amdgcn_ballot_w64(big) == 0) {
+      // Sorted on 32-bit keys: a candidate's order key with its low five bits
+      // replaced by 31 - its list slot (sign flipped for the signed sort;
+      // valid order keys exceed 2^23, so an empty lane's INT32_MIN sorts last).
+      // Lane t then reads its exact (key, 1023 - index) pair back from the
+      // list by that slot.  The short keys order the candidates exactly unless
+      // two of them differ only in the dropped bits, which the check below
+      // finds as an adjacent pair out of order; the wavefront then sorts the
+      // exact pairs.
+      int32_t c[G];
 #pragma unroll
-      for (int g = 0; g < G; ++g) v[g] = sort16_desc(v[g], q);
+      for (int g = 0; g < G; ++g)
+        c[g] = q < total[g] ? (int32_t)((((uint32_t)(v[g] >> 32) & ~31u) | (uint32_t)(31 - q)) ^ 0x80000000u)
+                            : INT32_MIN;
+      sort16_desc_g<G>(c, q);
+      bool bad = false;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        v[g] = q < total[g] ? cand[g][slot][31 - (c[g] & 31)] : 0;
+        const u32x2 b = __builtin_bit_cast(u32x2, v[g]);
+        const uint64_t next = __builtin_bit_cast(
+            uint64_t, u32x2{(uint32_t)__builtin_amdgcn_update_dpp(0, (int)b.x, 0x101, 0xF, 0xF, true),
+                            (uint32_t)__builtin_amdgcn_update_dpp(0, (int)b.y, 0x101, 0xF, 0xF, true)});  // row_shl:1
+        bad = bad || (q < total[g] && v[g] <= next);
+      }
+      if (__builtin_amdgcn_ballot_w64(bad) != 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) v[g] = sort16_desc(v[g], q);
+      }
     } else {
       // a row of this wavefront has 17..32 candidates: lane q also takes
       // candidate q + 16, both lists are sorted, and lane t keeps the larger
