@@ -495,6 +495,10 @@ template <int CTRL>
 __device__ __forceinline__ int32_t dpp_i32(int32_t v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
 }
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, dpp_i32<CTRL>(__builtin_bit_cast(int32_t, v)));
+}
 // Compare-exchange of one sorting stage: the lane keeps the larger value
 // unless (p & BIT), CTRL naming the partner (p ^ 1, p ^ 3, p ^ 7, p ^ 15 or
 // p ^ 2).
@@ -809,9 +813,22 @@ __global__ void __launch_bounds__(kFilterBlock) filter_kernel(const void* __rest
       const float val = float_of_key((uint32_t)(v[g] >> 32));
       const float v0 = row_bcast_f<0>(val);
       const float et = q < k ? exp_nonpos(val - v0) : 0.f;  // val <= v0, the row maximum
-      float e[KMAX];
-      bcast_all(et, e, std::make_integer_sequence<int, KMAX>{});
-      const float sum = np_sum<KMAX>(e, k);
+      float sum;
+      if constexpr (EIGHTH) {
+        // np_sum's order for 8 terms, ((e0 + e1) + (e2 + e3)) + ((e4 + e5) +
+        // (e6 + e7)), as a tree over lanes 0..7, each level adding the partial
+        // sum of the partner lane (p ^ 1, p ^ 2, then the other quad of the
+        // half): addition commutes, so every lane of the half ends with the
+        // same bits.
+        sum = et;
+        sum += dpp_f32<0xB1>(sum);
+        sum += dpp_f32<0x4E>(sum);
+        sum += dpp_f32<0x141>(sum);
+      } else {
+        float e[KMAX];
+        bcast_all(et, e, std::make_integer_sequence<int, KMAX>{});
+        sum = np_sum<KMAX>(e, k);
+      }
       const int64_t r = r0 + g * ROWS + slot;
       if (live[g] && q < k) {
         store_weight<DT>(weights, r * k + q, et / sum);
