@@ -20,9 +20,9 @@ static uint32_t key_of_bits(uint32_t b) {
 static uint32_t key_of_finite(uint32_t b) {
   const uint32_t sm = (uint32_t)((int32_t)b >> 31);
 #ifdef PLANT_DROPPED_SUBTRACT
-  return b ^ (sm & 0x7FFFFFFFu) ^ 0x80000000u;
+  return b ^ (sm | 0x80000000u);
 #else
-  return (b ^ (sm & 0x7FFFFFFFu) ^ 0x80000000u) - sm;
+  return (b ^ (sm | 0x80000000u)) - sm;
 #endif
 }
 

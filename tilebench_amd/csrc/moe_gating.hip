@@ -68,12 +68,12 @@ __device__ __forceinline__ uint32_t key_of_bits(uint32_t b) {
   return mag > 0x7F800000u ? 0xFFFFFFFFu : key;
 }
 
-// key_of_bits for a finite value (no NaN check): with s the sign mask,
-// b ^ (s & 0x7FFFFFFF) ^ 0x80000000 minus s, i.e. 0x80000000 + |x| bits for
+// key_of_bits for a finite value (no NaN check): with s the sign mask (0 or
+// all ones), b ^ (s | 0x80000000) minus s, i.e. 0x80000000 + |x| bits for
 // x >= 0 and 0x80000000 - |x| bits for x < 0 (one bitop3 and one subtract).
 __device__ __forceinline__ uint32_t key_of_finite(uint32_t b) {
   const uint32_t sm = (uint32_t)((int32_t)b >> 31);
-  return (b ^ (sm & 0x7FFFFFFFu) ^ 0x80000000u) - sm;
+  return (b ^ (sm | 0x80000000u)) - sm;
 }
 
 __device__ __forceinline__ float float_of_key(uint32_t u) {
