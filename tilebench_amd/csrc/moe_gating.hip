@@ -678,16 +678,30 @@ __global__ void __launch_bounds__(kFilterBlock) filter_kernel(const void* __rest
 
   // candidate mask (bit j for element j), counts and their inclusive prefix
   // across the row's 16 lanes
+  // Below eight elements per lane the per-element compares are kept as they
+  // are (lane masks the gather branches on) and the count is their running sum.
+  constexpr bool FLAGS = !S::STAGED;
   uint32_t mask[G];
+  bool ge[G][FLAGS ? V : 1];
   int cnt[G], incl[G], total[G];
   bool fast = finite;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    uint32_t m = 0;
+    if constexpr (FLAGS) {
+      int c = 0;
 #pragma unroll
-    for (int j = V - 1; j >= 0; --j) m = m + m + (uint32_t)(f[g][j] >= T[g]);
-    mask[g] = live[g] ? m : 0u;  // rows past M (zeros) have no candidates: nothing is written for them
-    cnt[g] = __builtin_popcount(m);
+      for (int j = 0; j < V; ++j) {
+        ge[g][j] = f[g][j] >= T[g];
+        c += (int)ge[g][j];
+      }
+      cnt[g] = c;
+    } else {
+      uint32_t m = 0;
+#pragma unroll
+      for (int j = V - 1; j >= 0; --j) m = m + m + (uint32_t)(f[g][j] >= T[g]);
+      mask[g] = live[g] ? m : 0u;  // rows past M (zeros) have no candidates: nothing is written for them
+      cnt[g] = __builtin_popcount(m);
+    }
     int x = cnt[g];
     x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);  // row_shr:1
     x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);  // row_shr:2
@@ -733,14 +747,17 @@ __global__ void __launch_bounds__(kFilterBlock) filter_kernel(const void* __rest
     } else {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const int base = incl[g] - cnt[g];
+        // rows past M (zeros) have no candidates: nothing is written for them
+        int dst = incl[g] - cnt[g];
 #pragma unroll
-        for (int j = 0; j < V; ++j)
-          if ((mask[g] >> j) & 1u) {
+        for (int j = 0; j < V; ++j) {
+          if (live[g] && ge[g][j]) {
             const int idx = (j / EPC) * (LPR * EPC) + q * EPC + (j % EPC);
-            cand[g][slot][base + __builtin_popcount(mask[g] & ((1u << j) - 1u))] =
+            cand[g][slot][dst] =
                 ((uint64_t)key_of_finite(__builtin_bit_cast(uint32_t, f[g][j])) << 32) | (uint32_t)(1023 - idx);
           }
+          dst += (int)ge[g][j];
+        }
       }
     }
     // The lists are read by other lanes of this wavefront only (each
