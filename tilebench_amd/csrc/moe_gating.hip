@@ -11,21 +11,25 @@
 //      that is NaN exactly when an element is inf or NaN (a sum of x * 0);
 //   2. T = the k-th largest of the 16 lane maxima (a bitonic network across
 //      the row's lanes on their signed-int keys, each compare-exchange one
-//      max and one min with the partner read by DPP, and a select).  The k
-//      lanes with the largest maxima hold k distinct elements >= T, so the
-//      row's k-th largest element is >= T, and every element the top-k can
-//      select is >= T;
-//   3. the lane's candidates, elements >= T (float compare: -0 == +0), as a
-//      bit mask;
+//      max and one min with the partner read by DPP, and a select; for k = 8
+//      only the half sorts and a min over the eight largest, eighth_of16_g).
+//      The k lanes with the largest maxima hold k distinct elements >= T, so
+//      the row's k-th largest element is >= T, and every element the top-k
+//      can select is >= T;
+//   3. the lane's candidates, elements >= T (float compare: -0 == +0): with
+//      V >= 8 a bit mask, with V = 4 the compares themselves and their count;
 //   4. the row's candidates are compacted (prefix sum of the lane counts) into
 //      an LDS list of exact (key, 1023 - index) pairs (with V >= 8 by a loop
 //      over the mask's set bits, each value read back from an LDS copy of the
-//      lane's elements; with V = 4 by one masked write per element); with at most 16 of
-//      them, lane i takes candidate i and a bitonic network over the 16 lanes
-//      sorts them: lane t ends with the t-th selection.  With 17 to 32, lane i
-//      also takes candidate i + 16, both lists are sorted and merged (lane t
-//      keeps the larger of list 0's t-th and list 1's (15 - t)-th, a bitonic
-//      sequence holding the top 16, sorted by four half-cleaners).
+//      lane's elements; with V = 4 by one masked write per element); with at
+//      most 16 of them, lane i takes candidate i and a bitonic network over
+//      the 16 lanes sorts them on 32-bit keys that hold the list slot in
+//      their low bits, checked against the exact pairs read back by slot
+//      (the wavefront sorts the exact pairs when the check fails): lane t
+//      ends with the t-th selection.  With 17 to 32, lane i also takes
+//      candidate i + 16, both lists are sorted and merged (lane t keeps the
+//      larger of list 0's t-th and list 1's (15 - t)-th, a bitonic sequence
+//      holding the top 16, sorted by four half-cleaners).
 // On random logits a row has about 10 candidates at k = 8; 2.6 % of the
 // wavefronts at E = 256 (0.2 % at E = 64) have a row with more than 16, and
 // far fewer one with more than 32.  A wavefront any of whose rows has more
