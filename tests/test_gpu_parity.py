@@ -222,6 +222,57 @@ def test_gating_half_dtypes(gpu, dt):
     np.testing.assert_array_equal(ti.numpy(), ri)
 
 
+@pytest.mark.parametrize("E", [5, 16, 100, 120, 128, 1024])
+@pytest.mark.parametrize("k", [1, 2])
+@pytest.mark.parametrize("dt", ["fp16", "bf16"])
+def test_gating_top2_half_paths(gpu, E, k, dt):
+    """k <= 2 on half logits (the 32-bit selection): lanes with whole 16-byte
+    chunks (E = 128, 1024), lanes reading element by element (E = 5, 100, 120:
+    rows not a 16-byte multiple or a lane's chunk past the row's end), one lane
+    per row (E <= 16) and 64 (E = 1024); heavy ties, signed zeros, +-inf, all-
+    equal rows, and NaN rows that send their wavefront to the general path.
+    Indices exact; weights NaN where the oracle's are and otherwise within one
+    unit of the half's last place (the device expf and numpy's may differ by an
+    fp32 ulp, which the rounding to a half can carry, as in the filter test)."""
+    from tilebench_amd.benchmarks.operators.moe_topk_gating import impl_hip
+
+    _say("gating top2 half", E, k, dt)
+    tdt = torch.float16 if dt == "fp16" else torch.bfloat16
+    rng = np.random.default_rng(E * 10 + k)
+    x = rng.integers(-4, 5, size=(700, E)).astype(np.float32) * 0.5    # heavy ties
+    x[:300] = rng.standard_normal((300, E)).astype(np.float32)
+    x[310, :] = 0.0
+    x[310, E // 2] = -0.0
+    x[311, :] = -0.0
+    x[312, :] = -np.inf
+    x[313, E - 1] = np.inf
+    x[314, 0] = np.inf
+    x[314, E // 2] = np.inf
+    x[315, :] = 1.5
+    x[330, E // 3] = np.nan                   # general path for its wavefront (the inf rows stay out of it)
+    x[650, 0] = np.nan
+    x[651, :] = np.nan
+    logits = torch.from_numpy(x).to(tdt)
+    w, i = impl_hip.run(logits.to(gpu), logits.shape[0], E, k)
+    torch.cuda.synchronize()
+    bits = logits.view(torch.int16).numpy().view(np.uint16) if dt == "bf16" else logits.numpy()
+    rw, ri = oracle.moe_topk_gating(bits, k, dtype=dt)
+    np.testing.assert_array_equal(i.cpu().numpy(), ri)
+    got = _u16(w)
+    want = np.asarray(rw).view(np.uint16)
+    nan_got = np.isnan(w.float().cpu().numpy())
+    nan_want = np.isnan(oracle.bf16_bits_to_f32(rw) if dt == "bf16" else rw.astype(np.float32))
+    np.testing.assert_array_equal(nan_got, nan_want)
+    assert np.abs(got[~nan_got].astype(np.int32) - want[~nan_want].astype(np.int32)).max() <= 1
+    # Bit for bit against the general path: the same logits in fp32 take it
+    # (k <= 2 in fp32 has no 32-bit shortcut), and its fp32 weights rounded
+    # once to the half dtype are what the half path stores.
+    w32, i32 = impl_hip.run(logits.float().to(gpu), logits.shape[0], E, k)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(i.cpu().numpy(), i32.cpu().numpy())
+    np.testing.assert_array_equal(got[~nan_got], _u16(w32.to(tdt))[~nan_got])
+
+
 @pytest.mark.parametrize("M", [1024, 20480])
 @pytest.mark.parametrize("dt", ["fp16", "bf16", "fp32"])
 def test_gating_reference_grid(gpu, M, dt):

@@ -49,6 +49,9 @@
 // xor-butterfly, which leaves every lane of the row with the winner, and the
 // lane that held it pops its list.  Selection runs on the logits themselves,
 // never on exp() values, so rounding in exp cannot create or break ties.
+// For k <= 2 on fp16/bf16 logits (the reference grid) the selection runs on
+// 32-bit (16-bit key, index) values instead (top2_half), falling back to the
+// doubles for a wavefront that holds a NaN.
 //
 // Key map: k(x) = 0x80000000 + |x| bits for x >= 0 and 0x80000000 - |x| bits
 // for x < 0, so -0.0 and +0.0 meet at 0x80000000 (they compare equal), and
@@ -353,6 +356,108 @@ __device__ __forceinline__ void write_selected(const double (&sel)[KMAX], int64_
   }
 }
 
+// k <= 2 on fp16 / bf16 logits without NaN: the selection in 32-bit integers.
+// A half's order key is 16 bits wide (the 32-bit key of its exact fp32 value,
+// shifted right by 16, for the same order and ties), so an element is one
+// uint32, key16 << 16 | (1023 - index), and no two elements of a row are
+// equal.  The keys of two halves come from packed 16-bit operations on the
+// loaded word (finite map: h ^ (s | 0x8000) - s, s the half's sign mask);
+// inf needs no special case, and a wavefront holding a NaN (whose key is the
+// largest) returns false for the general path.  Within a lane the low bits
+// hold 15 - j (element j of the lane's 16); the lane's part of 1023 - index,
+// 1008 - 16q, is ORed in after the lane's top two are found (pairs sorted,
+// then merged into the running pair).  The rows' top two follow from the
+// same merge across the LPR lanes (butterfly), and the outputs from the
+// general path's formulas: expf(v_t - v_0), the sum left to right, the
+// quotient rounded once to the logits dtype.
+template <int DT, int LPR>
+__device__ __forceinline__ bool top2_half(const void* __restrict__ logits, void* __restrict__ weights,
+                                          int32_t* __restrict__ indices, int64_t r, int q, int E, int k) {
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  constexpr int V = 16;
+  constexpr uint32_t NAN_MAG = DT == 1 ? 0x7C00u : 0x7F80u;  // |h| above this is NaN
+  const int c0 = q * V;
+  uint32_t m1 = 0, m2 = 0;  // the lane's top two, m1 > m2 (0: none)
+  bool nan = false;
+  auto put2 = [&](uint32_t a, uint32_t b) {  // merge two elements into (m1, m2)
+    const uint32_t hi = a > b ? a : b, lo = a > b ? b : a;
+    const uint32_t x = m1 < hi ? m1 : hi;
+    m1 = m1 > hi ? m1 : hi;
+    m2 = m2 > lo ? m2 : lo;
+    m2 = m2 > x ? m2 : x;
+  };
+  const bool aligned16 = ((E * 2) & 15) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0;
+  if (c0 + V <= E && aligned16) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(logits) + r * E + c0);
+    const u32x4 x0 = __builtin_nontemporal_load(p), x1 = __builtin_nontemporal_load(p + 1);
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[i] = x0[i];
+      w[4 + i] = x1[i];
+    }
+    u16x2 mag = {0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const u16x2 mi = __builtin_bit_cast(u16x2, w[i] & 0x7FFF7FFFu);
+      mag = __builtin_elementwise_max(mag, mi);
+      const uint32_t sm = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s16x2, w[i]) >> (short)15);
+      const uint32_t key = __builtin_bit_cast(
+          uint32_t, __builtin_bit_cast(u16x2, w[i] ^ (sm | 0x80008000u)) - __builtin_bit_cast(u16x2, sm));
+      // element 2i in the low half, 2i + 1 in the high half
+      put2((key << 16) | (uint32_t)(15 - 2 * i), (key & 0xFFFF0000u) | (uint32_t)(14 - 2 * i));
+    }
+    nan = mag.x > NAN_MAG || mag.y > NAN_MAG;
+  } else {
+    const uint16_t* rowp = reinterpret_cast<const uint16_t*>(logits) + r * E;
+#pragma unroll
+    for (int j = 0; j < V; j += 2) {
+      uint32_t c[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int e = c0 + j + h;
+        const uint32_t b = e < E ? rowp[e] : 0u;
+        const uint32_t sm = (b & 0x8000u) ? 0xFFFFu : 0u;
+        nan = nan || (e < E && (b & 0x7FFFu) > NAN_MAG);
+        c[h] = e < E ? ((((b ^ (sm | 0x8000u)) - sm) & 0xFFFFu) << 16) | (uint32_t)(15 - j - h) : 0u;
+      }
+      put2(c[0], c[1]);
+    }
+  }
+  if (__builtin_amdgcn_ballot_w64(nan) != 0) return false;
+  const uint32_t lane_rev = 1008u - 16u * (uint32_t)q;  // 1023 - (c0 + j) = lane_rev | (15 - j)
+  m1 = m1 != 0 ? m1 | lane_rev : 0u;
+  m2 = m2 != 0 ? m2 | lane_rev : 0u;
+#pragma unroll
+  for (int step = 0; (1 << step) < LPR; ++step) {
+    const uint32_t p1 = xchg<LPR>(m1, step), p2 = xchg<LPR>(m2, step);
+    const uint32_t x = m1 < p1 ? m1 : p1;
+    m1 = m1 > p1 ? m1 : p1;
+    m2 = m2 > p2 ? m2 : p2;
+    m2 = m2 > x ? m2 : x;
+  }
+  // fp32 values of the two selections from their 16-bit keys
+  auto value = [](uint32_t m) {
+    const uint32_t kk = m >> 16;
+    const uint32_t h = kk >= 0x8000u ? kk - 0x8000u : 0x8000u | (0x8000u - kk);
+    if constexpr (DT == 1) return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+    return __builtin_bit_cast(float, h << 16);
+  };
+  const float v0 = value(m1);
+  const float e0 = expf(v0 - v0), e1 = k > 1 ? expf(value(m2) - v0) : 0.f;
+  const float sum = k > 1 ? e0 + e1 : e0;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    if (t < k && (LPR == 1 ? q == 0 : q == t)) {
+      const uint32_t m = t == 0 ? m1 : m2;
+      store_weight<DT>(weights, r * k + t, (t == 0 ? e0 : e1) / sum);
+      indices[r * k + t] = 1023 - (int)(m & 0xFFFFu);
+    }
+  }
+  return true;
+}
+
 template <int DT, int V, int LPR, int KMAX>
 __global__ void __launch_bounds__(kBlock) gating_kernel(const void* __restrict__ logits, void* __restrict__ weights,
                                                         int32_t* __restrict__ indices, int64_t M, int E, int k) {
@@ -361,6 +466,9 @@ __global__ void __launch_bounds__(kBlock) gating_kernel(const void* __restrict__
   const int64_t r = (int64_t)blockIdx.x * ROWS + threadIdx.x / LPR;
   const int q = threadIdx.x % LPR;
   if (r >= M) return;  // whole LPR groups leave together
+  if constexpr (KMAX == 2 && DT != 0 && V == 16) {
+    if (top2_half<DT, LPR>(logits, weights, indices, r, q, E, k)) return;
+  }
 
   // Keys of this lane's elements: one 16-byte load when the chunk lies inside
   // the row and rows are 16-byte multiples (so the load is aligned), else
