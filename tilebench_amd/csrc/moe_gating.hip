@@ -445,7 +445,8 @@ __device__ __forceinline__ bool top2_half(const void* __restrict__ logits, void*
     return __builtin_bit_cast(float, h << 16);
   };
   const float v0 = value(m1);
-  const float e0 = expf(v0 - v0), e1 = k > 1 ? expf(value(m2) - v0) : 0.f;
+  // expf(v0 - v0): 1 for finite v0, NaN for an infinite one (inf - inf)
+  const float e0 = (v0 - v0) + 1.f, e1 = k > 1 ? expf(value(m2) - v0) : 0.f;
   const float sum = k > 1 ? e0 + e1 : e0;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
