@@ -335,6 +335,7 @@ __device__ __forceinline__ void write_selected(const double (&sel)[KMAX], int64_
   float e[KMAX];
 #pragma unroll
   for (int t = 0; t < KMAX; ++t) e[t] = t < k ? expf(float_of_key(elem_key(sel[t])) - v0) : 0.f;
+  e[0] = (v0 - v0) + 1.f;  // expf(v0 - v0): 1, or NaN for an infinite v0 (inf - inf)
   const float sum = np_sum<KMAX>(e, k);
   const int64_t out0 = r * k;
   constexpr int SLOTS = (KMAX + LPR - 1) / LPR;
